@@ -1,0 +1,133 @@
+/*
+ * moe_mi355x.h -- C ABI of the MI355X (gfx950) Qwen3-MoE FP8 expert hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as
+ * void*), enqueues its kernels on that stream and returns 0 on success or a
+ * MOE_ERR_* code (or a hipError_t, which is positive) on failure.  No entry point
+ * synchronises the stream or allocates device memory; scratch comes in through a
+ * caller-owned workspace whose size the matching *_workspace_bytes() call returns.
+ *
+ * Layouts (row-major, C-contiguous, 16-byte aligned):
+ *   bf16  = uint16 bit patterns of bfloat16
+ *   fp8   = uint8 OCP e4m3fn codes (torch.float8_e4m3fn)
+ *   ids   = int32 or int64 (id_bytes = 4 or 8), [T, k]
+ *
+ * The reference path these replace lives in the reference server's dependency
+ * `transformers` 5.15.0 (reference pyproject.toml:14; TF = transformers/):
+ *   TF/models/qwen3_moe/modeling_qwen3_moe.py, TF/integrations/moe.py,
+ *   TF/integrations/finegrained_fp8.py.  It is reached from the reference at
+ *   src/inference_server/backends/torch_backend.py:38-40 (model load) and
+ *   :288-290, :313-320 (every model forward).
+ */
+#ifndef MOE_MI355X_H
+#define MOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MOE_OK = 0,
+  MOE_ERR_INVALID_ARG = -1,    /* null pointer, bad size or unsupported shape */
+  MOE_ERR_WORKSPACE = -2,      /* workspace smaller than *_workspace_bytes() */
+  MOE_ERR_ALIGNMENT = -3,      /* a pointer is not 16-byte aligned */
+};
+
+/* Human-readable text for a return code (MOE_ERR_* or hipError_t). */
+const char* moe_mi355x_error_string(int code);
+
+/* Library version, (major << 16) | minor. */
+int moe_mi355x_version(void);
+
+/*
+ * Router: logits = x @ w_router^T (bf16 out, fp32 accumulation), softmax in fp32,
+ * top-k by (descending logit, ascending expert id), optional renormalisation,
+ * weights cast to bf16.
+ * Replaces Qwen3MoeTopKRouter.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267.
+ *   x        bf16 [T, H]        w_router bf16 [E, H]
+ *   logits   bf16 [T, E] (out)  ids [T, k] (out, id_bytes)  weights bf16 [T, k] (out)
+ * Constraints: H % 32 == 0, 1 <= E <= 256, 1 <= k <= min(E, 32).
+ */
+size_t moe_mi355x_route_workspace_bytes(int T, int H, int E);
+int moe_mi355x_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                     void* logits, void* ids, int id_bytes, void* weights,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Softmax + top-k + renorm from given bf16 logits (the second half of moe_mi355x_route).
+ * Replaces modeling_qwen3_moe.py:261-266.
+ */
+int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, int renorm,
+                            void* ids, int id_bytes, void* weights, void* stream);
+
+/*
+ * Stable expert sort of the T*k (token, slot) pairs plus per-expert counts, offsets
+ * and the M-tile list the grouped GEMMs walk.
+ * Replaces torch.sort + histc + cumsum, TF/integrations/moe.py:389-403.
+ *   ids     [T*k] (id_bytes), values in [0, E)
+ *   perm    int32 [T*k]   (out) flat pair index t*k+j in sorted order (stable)
+ *   counts  int32 [E]     (out) pairs per expert (the reference's tokens_per_expert)
+ *   offsets int32 [E+1]   (out) exclusive prefix; offsets[1:] is the reference's cumsum
+ *   tiles   int32 [max_tiles, 4] (out) {expert, first sorted row, rows, 0} per block_m rows
+ *   n_tiles int32 [1]     (out)
+ * max_tiles = moe_mi355x_align_max_tiles(T*k, E, block_m).
+ */
+int moe_mi355x_align_max_tiles(int S, int E, int block_m);
+size_t moe_mi355x_align_workspace_bytes(int S, int E);
+int moe_mi355x_align(const void* ids, int id_bytes, int T, int k, int E, int block_m,
+                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles,
+                     int32_t* n_tiles, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Dynamic activation quantisation, per row and per 128-column group:
+ * s = amax/448 (1 if amax == 0), q = e4m3(clamp(x/s, -448, 448)).
+ * Replaces the inline activation quantiser of the FP8 grouped GEMM,
+ * TF/integrations/finegrained_fp8.py:191-196 (Triton source not shipped).
+ *   x bf16 [R, C] -> q fp8 [R, C], scales fp32 [R, C/128].  C % 128 == 0.
+ */
+int moe_mi355x_quantize_act_fp8(const void* x, int R, int C, void* q, float* scales, void* stream);
+
+/*
+ * Weight quantisation per 128x128 tile: scale = 448/amax (1 if amax == 0),
+ * q = e4m3(clamp(w*scale, -448, 448)), scale_inv = 1/scale.
+ * Replaces Fp8Quantize._quantize_one, TF/integrations/finegrained_fp8.py:903-941.
+ *   w [B, N, K] (w_dtype 0 = bf16, 1 = fp32) -> q fp8 [B, N, K], scale_inv fp32 [B, N/128, K/128]
+ */
+int moe_mi355x_quantize_weight_fp8(const void* w, int w_dtype, int B, int N, int K,
+                                   void* q, float* scale_inv, void* stream);
+
+/*
+ * FP8 block-scaled experts forward.
+ * Replaces fp8_grouped_mm_experts_forward, TF/integrations/finegrained_fp8.py:498-589
+ * (signature forward(self, hidden_states, top_k_index, top_k_weights)).
+ *   x        bf16 [T, H]          ids [T, k] (id_bytes)      weights bf16 [T, k]
+ *   w13      fp8 [E, 2I, H]       s13 fp32 [E, 2I/128, H/128]   (gate rows [0,I), up rows [I,2I))
+ *   w2       fp8 [E, H, I]        s2  fp32 [E, H/128, I/128]
+ *   out      bf16 [T, H]
+ * Constraints: H % 128 == 0, I % 128 == 0, 1 <= E <= 256, 1 <= k <= 32.
+ */
+size_t moe_mi355x_experts_workspace_bytes(int T, int H, int I, int E, int k);
+int moe_mi355x_experts_fp8(const void* x, const void* ids, int id_bytes, const void* weights,
+                           int T, int H, int I, int E, int k,
+                           const void* w13, const float* s13, const void* w2, const float* s2,
+                           void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Whole MoE block: router + FP8 experts.
+ * Replaces Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
+ * logits / ids / weights may be NULL when the caller does not need them.
+ */
+size_t moe_mi355x_block_workspace_bytes(int T, int H, int I, int E, int k);
+int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                         int renorm, const void* w13, const float* s13, const void* w2,
+                         const float* s2, void* out, void* logits, void* ids, int id_bytes,
+                         void* weights, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_MI355X_H */

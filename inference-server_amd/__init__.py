@@ -1,0 +1,35 @@
+"""MI355X (gfx950) Qwen3-MoE FP8 expert hot path.
+
+Importable as ``inference_server_amd`` (the on-disk folder name carries a hyphen;
+``__graft_entry__.load_package()`` registers it under that module name).
+
+Layers:
+  ``_lib``     ctypes binding of ``libmoe_mi355x.so`` (C ABI: ``include/moe_mi355x.h``)
+  ``kernels``  torch-tensor wrappers of every entry point
+  ``experts``  drop-in modules and the transformers experts-interface registration
+  ``build``    hipcc build of the library
+"""
+
+from __future__ import annotations
+
+from . import _lib, kernels  # noqa: F401
+from .experts import (  # noqa: F401
+    IMPLEMENTATION_KEY,
+    MI355XFp8Experts,
+    MI355XSparseMoeBlock,
+    MI355XTopKRouter,
+    mi355x_fp8_experts_forward,
+    register,
+    swap_moe_blocks,
+)
+from .kernels import (  # noqa: F401
+    align,
+    experts_fp8,
+    moe_block_fp8,
+    quantize_act_fp8,
+    quantize_weight_fp8,
+    route,
+    topk_softmax,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,240 @@
+// Expert sort / align: stable counting sort of the T*k (token, slot) pairs by
+// expert id, per-expert counts and offsets, and the block_m-row tile list the
+// grouped GEMMs iterate over.
+//
+// Reference: TF/integrations/moe.py:389-403 (torch.sort, histc, cumsum).
+//
+// Stability comes from wave ballots: lanes holding the same expert id are
+// found with one ballot per id bit, a lane's rank among them is the popcount of
+// that mask below its own lane, and per-wave totals are scanned in LDS in wave
+// order.  Pairs are processed in 1024-pair chunks in index order, so the result
+// equals a stable argsort.
+//
+// Ids outside [0, E) are expert-parallel sentinels (moe.py:405-419): they are left
+// out of counts and tiles and placed, stably, after offsets[E] at the tail of perm.
+#include "common.h"
+
+namespace {
+
+constexpr int kChunk = 1024;       // pairs per chunk == threads per workgroup
+constexpr int kWaves = kChunk / MOE_WAVE;
+constexpr int kMaxE = 256;
+constexpr int kBuckets = kMaxE + 1;  // experts plus the sentinel bucket
+
+__device__ __forceinline__ int bucket_of(const void* ids, int id_bytes, int i, int E) {
+  const long r = id_bytes == 8 ? (long)((const int64_t*)ids)[i] : (long)((const int32_t*)ids)[i];
+  return (r < 0 || r >= E) ? E : (int)r;
+}
+constexpr int kSingleMaxS = 4096;  // above this the three-kernel path is used
+
+// Exclusive scans of counts and of ceil(count / block_m) over experts; wave 0 of the block.
+__device__ void scan_counts(const int* s_cnt, int E, int block_m, int* s_off, int* s_toff) {
+  const int lane = threadIdx.x & 63;
+  if ((threadIdx.x >> 6) != 0) return;
+  int c[4], t[4], sc = 0, st = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = lane * 4 + q;
+    c[q] = e < E ? s_cnt[e] : 0;
+    t[q] = (c[q] + block_m - 1) / block_m;
+    sc += c[q];
+    st += t[q];
+  }
+  int ic = sc, it = st;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int oc = __shfl_up(ic, d, MOE_WAVE), ot = __shfl_up(it, d, MOE_WAVE);
+    if (lane >= d) {
+      ic += oc;
+      it += ot;
+    }
+  }
+  int ec = ic - sc, et = it - st;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = lane * 4 + q;
+    if (e < E) {
+      s_off[e] = ec;
+      s_toff[e] = et;
+    }
+    ec += c[q];
+    et += t[q];
+  }
+  if (lane == 63) {
+    s_off[E] = ic;
+    s_toff[E] = it;
+  }
+}
+
+// Writes counts, offsets and the tile list from the scanned LDS arrays.
+__device__ void emit_meta(const int* s_cnt, const int* s_off, const int* s_toff, int E, int block_m,
+                          int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles) {
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    offsets[e] = s_off[e];
+    if (e == E) {
+      n_tiles[0] = s_toff[E];
+      continue;
+    }
+    const int c = s_cnt[e];
+    counts[e] = c;
+    int tix = s_toff[e];
+    for (int r = 0; r < c; r += block_m, ++tix) {
+      int4 v = make_int4(e, s_off[e] + r, min(block_m, c - r), 0);
+      *(int4*)(tiles + 4 * tix) = v;
+    }
+  }
+}
+
+// Stable placement of one chunk of pairs [chunk0, chunk0 + 1024).  s_base holds the
+// next free sorted slot of every expert and is advanced by the chunk's counts.
+__device__ void scatter_chunk(const void* ids, int id_bytes, int S, int E, int chunk0, int* s_base,
+                              int (*s_wcnt)[kBuckets], int32_t* perm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = chunk0 + threadIdx.x;
+  const bool valid = i < S;
+  const int e = valid ? bucket_of(ids, id_bytes, i, E) : E + 1;  // E + 1 marks a lane with no pair
+  for (int x = lane; x <= E; x += MOE_WAVE) s_wcnt[wave][x] = 0;
+  __syncthreads();
+  uint64_t mask = __ballot(1);
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bal = __ballot(bit);
+    mask &= bit ? bal : ~bal;
+  }
+  const int rank = __popcll(mask & lanemask_lt());
+  if (valid && rank == 0) s_wcnt[wave][e] = __popcll(mask);
+  __syncthreads();
+  if (valid) {
+    int prefix = 0;
+    for (int w = 0; w < wave; ++w) prefix += s_wcnt[w][e];
+    perm[s_base[e] + prefix + rank] = i;
+  }
+  __syncthreads();
+  for (int x = threadIdx.x; x <= E; x += blockDim.x) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += s_wcnt[w][x];
+    s_base[x] += tot;
+  }
+  __syncthreads();
+}
+
+// Whole align in one workgroup (small S: decode batches).
+__global__ __launch_bounds__(kChunk) void align_single_kernel(const void* ids, int id_bytes, int S, int E,
+                                                              int block_m, int32_t* perm, int32_t* counts,
+                                                              int32_t* offsets, int32_t* tiles,
+                                                              int32_t* n_tiles) {
+  __shared__ int s_cnt[kBuckets];
+  __shared__ int s_off[kBuckets];
+  __shared__ int s_toff[kBuckets];
+  __shared__ int s_wcnt[kWaves][kBuckets];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_cnt[e] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < S; i += blockDim.x) atomicAdd(&s_cnt[bucket_of(ids, id_bytes, i, E)], 1);
+  __syncthreads();
+  scan_counts(s_cnt, E, block_m, s_off, s_toff);
+  __syncthreads();
+  emit_meta(s_cnt, s_off, s_toff, E, block_m, counts, offsets, tiles, n_tiles);
+  // s_off doubles as the running base from here on; s_off[E] starts the sentinel tail
+  for (int c0 = 0; c0 < S; c0 += kChunk) scatter_chunk(ids, id_bytes, S, E, c0, s_off, s_wcnt, perm);
+}
+
+// Large S, pass 1: per-chunk histograms  bc[b, e].
+__global__ __launch_bounds__(kChunk) void align_count_kernel(const void* ids, int id_bytes, int S, int E,
+                                                             int32_t* bc) {
+  __shared__ int s_cnt[kBuckets];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_cnt[e] = 0;
+  __syncthreads();
+  const int i = blockIdx.x * kChunk + threadIdx.x;
+  if (i < S) atomicAdd(&s_cnt[bucket_of(ids, id_bytes, i, E)], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) bc[(long)blockIdx.x * (E + 1) + e] = s_cnt[e];
+}
+
+// Large S, pass 2 (one workgroup): totals, offsets, tile list, and each chunk's
+// starting slot per expert, written back over bc.
+__global__ __launch_bounds__(kChunk) void align_scan_kernel(int32_t* bc, int nb, int E, int block_m,
+                                                            int32_t* counts, int32_t* offsets, int32_t* tiles,
+                                                            int32_t* n_tiles) {
+  __shared__ int s_cnt[kBuckets];
+  __shared__ int s_off[kBuckets];
+  __shared__ int s_toff[kBuckets];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    int tot = 0;
+    for (int b = 0; b < nb; ++b) tot += bc[(long)b * (E + 1) + e];
+    s_cnt[e] = tot;
+  }
+  __syncthreads();
+  scan_counts(s_cnt, E, block_m, s_off, s_toff);
+  __syncthreads();
+  emit_meta(s_cnt, s_off, s_toff, E, block_m, counts, offsets, tiles, n_tiles);
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    int run = s_off[e];
+    for (int b = 0; b < nb; ++b) {
+      const int c = bc[(long)b * (E + 1) + e];
+      bc[(long)b * (E + 1) + e] = run;
+      run += c;
+    }
+  }
+}
+
+// Large S, pass 3: stable placement of chunk b starting from its per-expert slots.
+__global__ __launch_bounds__(kChunk) void align_scatter_kernel(const void* ids, int id_bytes, int S, int E,
+                                                               const int32_t* bases, int32_t* perm) {
+  __shared__ int s_base[kBuckets];
+  __shared__ int s_wcnt[kWaves][kBuckets];
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_base[e] = bases[(long)blockIdx.x * (E + 1) + e];
+  __syncthreads();
+  scatter_chunk(ids, id_bytes, S, E, blockIdx.x * kChunk, s_base, s_wcnt, perm);
+}
+
+}  // namespace
+
+extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m) {
+  if (S <= 0 || E <= 0 || block_m <= 0) return 0;
+  return S / block_m + (S < E ? S : E);
+}
+
+extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E) {
+  if (S <= kSingleMaxS) return 0;
+  const size_t nb = (S + kChunk - 1) / kChunk;
+  return moe_align_up(nb * (E + 1) * sizeof(int32_t), 256);
+}
+
+int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
+                     int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles, void* workspace,
+                     size_t workspace_bytes, hipStream_t s) {
+  if (S <= kSingleMaxS) {
+    hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(kChunk), 0, s, ids, id_bytes, S, E, block_m, perm,
+                       counts, offsets, tiles, n_tiles);
+    MOE_CHECK_LAUNCH();
+    return MOE_OK;
+  }
+  MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_align_workspace_bytes(S, E), MOE_ERR_WORKSPACE);
+  const int nb = (S + kChunk - 1) / kChunk;
+  int32_t* bc = (int32_t*)workspace;
+  hipLaunchKernelGGL(align_count_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E, bc);
+  MOE_CHECK_LAUNCH();
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kChunk), 0, s, bc, nb, E, block_m, counts, offsets,
+                     tiles, n_tiles);
+  MOE_CHECK_LAUNCH();
+  hipLaunchKernelGGL(align_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
+                     (const int32_t*)bc, perm);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+extern "C" int moe_mi355x_align(const void* ids, int id_bytes, int T, int k, int E, int block_m,
+                                int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles,
+                                int32_t* n_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(T < 0 || k < 1 || E < 1 || E > kMaxE || block_m < 1, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(id_bytes != 4 && id_bytes != 8, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!counts || !offsets || !n_tiles, MOE_ERR_INVALID_ARG);
+  const long S = (long)T * k;
+  MOE_RETURN_IF(S > (1L << 30), MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(S > 0 && (!ids || !perm || !tiles), MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!moe_aligned16(tiles), MOE_ERR_ALIGNMENT);
+  return moe_launch_align(ids, id_bytes, (int)S, E, block_m, perm, counts, offsets, tiles, n_tiles, workspace,
+                          workspace_bytes, (hipStream_t)stream);
+}

@@ -1,0 +1,129 @@
+// Shared device helpers for the gfx950 MoE kernels: bf16 / e4m3 conversions,
+// wave64 reductions and the MFMA operand types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_mi355x.h"
+
+#define MOE_WAVE 64
+#define MOE_GROUP 128      // quantisation group / block size
+#define MOE_FP8_MAX 448.0f
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32 (bit patterns carried as uint16)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------------------
+// fp32 -> OCP e4m3fn.  Inputs are clamped to [-448, 448] by the callers, so the
+// conversion only has to round (to nearest even, the hardware default mode).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  int both = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+  return (uint32_t)both;
+}
+
+__device__ __forceinline__ float clamp_fp8(float v) {
+  return fminf(fmaxf(v, -MOE_FP8_MAX), MOE_FP8_MAX);
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (butterfly over all 64 lanes; every lane gets the result)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, MOE_WAVE));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, MOE_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    uint32_t o = (uint32_t)__shfl_xor((int)v, m, MOE_WAVE);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// max over aligned groups of `width` lanes (width a power of two <= 64)
+template <int WIDTH>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, MOE_WAVE));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int lane = __lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Read an expert id stored as int32 or int64.
+__device__ __forceinline__ int load_id(const void* ids, int id_bytes, int i) {
+  return id_bytes == 8 ? (int)((const int64_t*)ids)[i] : ((const int32_t*)ids)[i];
+}
+
+// ---------------------------------------------------------------------------
+// Host-side helpers shared by the entry points
+// ---------------------------------------------------------------------------
+static inline size_t moe_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+static inline bool moe_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+#define MOE_CHECK_LAUNCH()                          \
+  do {                                              \
+    hipError_t _e = hipGetLastError();              \
+    if (_e != hipSuccess) return (int)_e;           \
+  } while (0)
+
+#define MOE_RETURN_IF(cond, code) \
+  do {                            \
+    if (cond) return (code);      \
+  } while (0)
+
+// Workspace carving: successive 256-byte aligned slices of one caller buffer.
+struct WsCarver {
+  char* base;
+  size_t off;
+  __host__ explicit WsCarver(void* b) : base((char*)b), off(0) {}
+  template <typename T>
+  __host__ T* take(size_t count) {
+    off = moe_align_up(off, 256);
+    T* p = base ? (T*)(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+// Internal launchers shared between translation units.
+int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hipStream_t s);
+int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
+                     int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                     void* workspace, size_t workspace_bytes, hipStream_t s);

@@ -1,0 +1,224 @@
+// Grouped FP8 (e4m3) GEMMs with 128x128 block scales on gfx950 MFMA.
+//
+//   MODE_GATE_UP: y = xq[token(pair)] @ W13[e]^T, epilogue h = silu(gate) * up in
+//                 the reference's bf16 rounding order, written per sorted row.
+//                 (TF/integrations/finegrained_fp8.py:547-563 + moe.py:509-520)
+//   MODE_DOWN:    z = hq[row] @ W2[e]^T, epilogue bf16(z) * routing weight (bf16),
+//                 written at the pair's original position t*k+j, which folds the
+//                 reference's inverse permutation (finegrained_fp8.py:565-583).
+//
+// One v_mfma_f32_16x16x128_f8f6f4 consumes exactly one 128-deep K block, so the
+// two fp32 block scales (activation row scale x weight tile scale) are applied
+// once per MFMA result: acc += mfma(a, b, 0) * (sa[row, kb] * sw[nblk, kb]).
+//
+// Operand layout: lane l supplies row (l % 16) of its operand and bytes
+// [32 * (l / 16), 32 * (l / 16) + 32) of the 128-byte K block, for A and for B
+// alike, so every product pairs matching K indices.  The 16x16 fp32 result holds
+// D[4 * (l / 16) + q][l % 16] in element q of lane l.
+//
+// Workgroup = 4 waves = (4 / KS) column groups x KS K-splits.  A wave owns 16
+// output columns (for gate_up: 16 gate rows + the matching 16 up rows of W13)
+// and WM 16-row M fragments of one expert tile.  K-split partials are summed
+// through LDS in a fixed order (deterministic).  Each weight byte is read once
+// per M tile, straight from HBM into VGPRs: the decode case is a weight stream.
+#include "common.h"
+
+namespace {
+
+enum { MODE_GATE_UP = 0, MODE_DOWN = 1 };
+
+struct GemmArgs {
+  const uint8_t* a;        // gate_up: xq [T, K] (rows are tokens); down: hq [S, K] (sorted rows)
+  const float* sa;         // activation scales, [rows, K/128]
+  const uint8_t* w;        // [E, Nw, K]
+  const float* sw;         // [E, Nw/128, K/128]
+  const int32_t* perm;     // [S] sorted row -> flat pair index
+  const int32_t* tiles;    // [max_tiles, 4] {expert, first sorted row, rows, 0}
+  const int32_t* n_tiles;  // [1]
+  const uint16_t* topk_w;  // down: routing weights bf16 [S] by flat pair
+  uint16_t* out;           // gate_up: h [S, N]; down: pair outputs [S, N]
+  int K;                   // reduction length
+  int N;                   // output columns (gate_up: I, down: H)
+  int topk;                // k, for pair -> token
+};
+
+constexpr int kMaxKB = 32;  // K <= 4096
+
+template <int MODE, int WM, int KS>
+__global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
+  constexpr int CG = 4 / KS;                  // column groups per workgroup
+  constexpr int NOP = MODE == MODE_GATE_UP ? 2 : 1;  // B operands per wave (gate, up)
+  constexpr int BM = 16 * WM;
+
+  const int tile = blockIdx.x;
+  if (tile >= p.n_tiles[0]) return;  // workgroup-uniform
+  const int4 ti = *(const int4*)(p.tiles + 4 * tile);
+  const int e = ti.x, row0 = ti.y, rows = ti.z;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cg = wave % CG, ks = wave / CG;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int KB = p.K / MOE_GROUP;
+  const int n0 = (blockIdx.y * CG + cg) * 16;
+  const int Nw = MODE == MODE_GATE_UP ? 2 * p.N : p.N;
+
+  __shared__ int s_arow[BM];                 // activation row of each tile row
+  __shared__ float s_sa[BM][kMaxKB];         // activation scales of the tile
+  __shared__ float s_red[KS > 1 ? (KS - 1) * CG * WM * NOP * 4 * 64 : 1];
+
+  for (int r = threadIdx.x; r < BM; r += blockDim.x) {
+    const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
+    s_arow[r] = MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
+    const int r = i / KB, kb = i % KB;
+    s_sa[r][kb] = p.sa[(long)s_arow[r] * KB + kb];
+  }
+  __syncthreads();
+
+  const uint8_t* aptr[WM];
+#pragma unroll
+  for (int mi = 0; mi < WM; ++mi) aptr[mi] = p.a + (long)s_arow[mi * 16 + lr] * p.K + lg * 32;
+  const uint8_t* bptr[NOP];
+  const float* swp[NOP];
+#pragma unroll
+  for (int o = 0; o < NOP; ++o) {
+    const int wrow = n0 + o * p.N;  // up rows follow the I gate rows
+    bptr[o] = p.w + ((long)e * Nw + wrow + lr) * p.K + lg * 32;
+    swp[o] = p.sw + ((long)e * (Nw / MOE_GROUP) + wrow / MOE_GROUP) * KB;
+  }
+
+  v4f acc[WM][NOP];
+#pragma unroll
+  for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) acc[mi][o] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  v8i bc[NOP], ac[WM];
+  int kb = ks;
+  if (kb < KB) {
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) bc[o] = *(const v8i*)(bptr[o] + kb * MOE_GROUP);
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi) ac[mi] = *(const v8i*)(aptr[mi] + kb * MOE_GROUP);
+  }
+  for (; kb < KB; kb += KS) {
+    v8i bn[NOP], an[WM];
+    const int kn = kb + KS;
+    if (kn < KB) {
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) bn[o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi) an[mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
+    }
+    float swv[NOP];
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) swv[o] = swp[o][kb];
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi) {
+      float sav[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sav[q] = s_sa[mi * 16 + 4 * lg + q][kb];
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) {
+        const v4f zero = {0.f, 0.f, 0.f, 0.f};
+        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ac[mi], bc[o], zero, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[mi][o][q] = fmaf(t[q], sav[q] * swv[o], acc[mi][o][q]);
+      }
+    }
+    if (kn < KB) {
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) bc[o] = bn[o];
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi) ac[mi] = an[mi];
+    }
+  }
+
+  if constexpr (KS > 1) {
+    constexpr int PER = WM * NOP * 4;
+    if (ks > 0) {
+      float* dst = s_red + (((ks - 1) * CG + cg) * PER) * 64;
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int o = 0; o < NOP; ++o)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dst[((mi * NOP + o) * 4 + q) * 64 + lane] = acc[mi][o][q];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int s = 1; s < KS; ++s) {
+      const float* src = s_red + (((s - 1) * CG + cg) * PER) * 64;
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi)
+#pragma unroll
+        for (int o = 0; o < NOP; ++o)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[mi][o][q] += src[((mi * NOP + o) * 4 + q) * 64 + lane];
+    }
+  }
+
+  const int col = n0 + lr;
+#pragma unroll
+  for (int mi = 0; mi < WM; ++mi) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = mi * 16 + 4 * lg + q;
+      if (r >= rows) continue;
+      const int srow = row0 + r;
+      if constexpr (MODE == MODE_GATE_UP) {
+        // grouped GEMM output is bf16; silu(gate) rounds to bf16; the product rounds again
+        const float g = round_bf16(acc[mi][0][q]);
+        const float u = round_bf16(acc[mi][1][q]);
+        const float sg = round_bf16(g / (1.0f + expf(-g)));
+        p.out[(long)srow * p.N + col] = f32_to_bf16(sg * u);
+      } else {
+        const int pair = p.perm[srow];
+        const float z = round_bf16(acc[mi][0][q]);
+        const float wt = bf16_to_f32(p.topk_w[pair]);
+        p.out[(long)pair * p.N + col] = f32_to_bf16(z * wt);
+      }
+    }
+  }
+}
+
+template <int MODE, int WM, int KS>
+int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
+  constexpr int CG = 4 / KS;
+  dim3 grid(max_tiles, a.N / (16 * CG));
+  hipLaunchKernelGGL((grouped_gemm_fp8_kernel<MODE, WM, KS>), grid, dim3(256), 0, s, a);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+}  // namespace
+
+// Tile height (rows per M tile) the grouped GEMMs use for S pairs over E experts.
+int moe_gemm_block_m(int S, int E) {
+  return (S <= 16 * E) ? 16 : 64;
+}
+
+int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                             const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
+                             const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
+                             uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
+                             int block_m, hipStream_t s) {
+  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k};
+  int rc;
+  if (block_m == 16)
+    rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
+  else
+    rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
+  if (rc) return rc;
+  rc = moe_launch_quant_act(h, S, I, hq, sh, s);
+  if (rc) return rc;
+  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
+  if (block_m == 16)
+    rc = launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  else
+    rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
+  return rc;
+}

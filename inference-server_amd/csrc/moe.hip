@@ -1,0 +1,214 @@
+// Experts / block entry points: activation quantisation -> align -> gate_up GEMM
+// (fused SiLU*up) -> intermediate quantisation -> down GEMM (fused routing-weight
+// product and inverse permutation) -> deterministic top-k combine.
+//
+// Reference: fp8_grouped_mm_experts_forward, TF/integrations/finegrained_fp8.py:498-589,
+// and Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
+#include "common.h"
+
+int moe_gemm_block_m(int S, int E);
+int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                             const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
+                             const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
+                             uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
+                             int block_m, hipStream_t s);
+int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                     void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                     size_t workspace_bytes, hipStream_t s);
+extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E);
+extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m);
+extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E);
+
+namespace {
+
+// out[t, :] = bf16( sum_j pairs[t*k + j, :] ) with fp32 accumulation in slot order
+// (moe.py:476 view(T,k,H).sum(1)); sentinel slots (ids outside [0,E)) add zero.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ pairs, const void* ids,
+                                                      int id_bytes, int T, int k, int H, int E,
+                                                      uint16_t* __restrict__ out) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per_row = H / 8;
+  if (idx >= (long)T * per_row) return;
+  const int t = (int)(idx / per_row), c8 = (int)(idx % per_row);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < k; ++j) {
+    const int pr = t * k + j;
+    const long id = id_bytes == 8 ? (long)((const int64_t*)ids)[pr] : (long)((const int32_t*)ids)[pr];
+    if (id < 0 || id >= E) continue;
+    const uint4 v = *(const uint4*)(pairs + (long)pr * H + c8 * 8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += __uint_as_float(w[i] << 16);
+      acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  uint4 o;
+  o.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+  o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+  o.z = (uint32_t)f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+  o.w = (uint32_t)f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+  *(uint4*)(out + (long)t * H + c8 * 8) = o;
+}
+
+struct ExpertsWs {
+  uint8_t* xq;
+  float* sx;
+  int32_t* perm;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* tiles;
+  int32_t* n_tiles;
+  void* align_ws;
+  size_t align_ws_bytes;
+  uint16_t* h;
+  uint8_t* hq;
+  float* sh;
+  uint16_t* pairs;
+  size_t total;
+  int block_m;
+  int max_tiles;
+};
+
+ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
+  ExpertsWs w{};
+  const int S = T * k;
+  w.block_m = moe_gemm_block_m(S, E);
+  w.max_tiles = moe_mi355x_align_max_tiles(S, E, w.block_m);
+  WsCarver c(base);
+  w.xq = c.take<uint8_t>((size_t)T * H);
+  w.sx = c.take<float>((size_t)T * (H / MOE_GROUP));
+  w.perm = c.take<int32_t>(S);
+  w.counts = c.take<int32_t>(E);
+  w.offsets = c.take<int32_t>(E + 1);
+  w.tiles = c.take<int32_t>((size_t)4 * (w.max_tiles > 0 ? w.max_tiles : 1));
+  w.n_tiles = c.take<int32_t>(4);
+  w.align_ws_bytes = moe_mi355x_align_workspace_bytes(S, E);
+  w.align_ws = c.take<char>(w.align_ws_bytes);
+  w.h = c.take<uint16_t>((size_t)S * I);
+  w.hq = c.take<uint8_t>((size_t)S * I);
+  w.sh = c.take<float>((size_t)S * (I / MOE_GROUP));
+  w.pairs = c.take<uint16_t>((size_t)S * H);
+  w.total = moe_align_up(c.off, 256);
+  return w;
+}
+
+bool experts_args_ok(int T, int H, int I, int E, int k, int id_bytes) {
+  return T >= 0 && H > 0 && I > 0 && H % MOE_GROUP == 0 && I % MOE_GROUP == 0 && H <= 4096 && I <= 4096 &&
+         E >= 1 && E <= 256 && k >= 1 && k <= 32 && k <= E && (id_bytes == 4 || id_bytes == 8) &&
+         (long)T * k < (1L << 28);
+}
+
+int launch_experts(const void* x, const void* ids, int id_bytes, const void* weights, int T, int H, int I,
+                   int E, int k, const void* w13, const float* s13, const void* w2, const float* s2, void* out,
+                   const ExpertsWs& w, hipStream_t s) {
+  const int S = T * k;
+  int rc = moe_launch_quant_act(x, T, H, w.xq, w.sx, s);
+  if (rc) return rc;
+  rc = moe_launch_align(ids, id_bytes, S, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
+                        w.align_ws, w.align_ws_bytes, s);
+  if (rc) return rc;
+  rc = moe_launch_grouped_gemms(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2, w.perm, w.tiles,
+                                w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.hq, w.sh, w.pairs, S, H,
+                                I, k, w.block_m, s);
+  if (rc) return rc;
+  const long threads = (long)T * (H / 8);
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     (const uint16_t*)w.pairs, ids, id_bytes, T, k, H, E, (uint16_t*)out);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+bool experts_ptrs_ok(const void* x, const void* ids, const void* weights, const void* w13, const float* s13,
+                     const void* w2, const float* s2, const void* out) {
+  return x && ids && weights && w13 && s13 && w2 && s2 && out;
+}
+
+bool experts_aligned(const void* x, const void* w13, const void* w2, const void* out) {
+  return moe_aligned16(x) && moe_aligned16(w13) && moe_aligned16(w2) && moe_aligned16(out);
+}
+
+}  // namespace
+
+extern "C" const char* moe_mi355x_error_string(int code) {
+  switch (code) {
+    case MOE_OK: return "success";
+    case MOE_ERR_INVALID_ARG: return "invalid argument (null pointer, size or unsupported shape)";
+    case MOE_ERR_WORKSPACE: return "workspace missing or smaller than the *_workspace_bytes() size";
+    case MOE_ERR_ALIGNMENT: return "a tensor pointer is not 16-byte aligned";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}
+
+extern "C" int moe_mi355x_version(void) { return (0 << 16) | 1; }
+
+extern "C" size_t moe_mi355x_experts_workspace_bytes(int T, int H, int I, int E, int k) {
+  if (!experts_args_ok(T, H, I, E, k, 4)) return 0;
+  return carve_experts(nullptr, T, H, I, E, k).total;
+}
+
+extern "C" int moe_mi355x_experts_fp8(const void* x, const void* ids, int id_bytes, const void* weights, int T,
+                                      int H, int I, int E, int k, const void* w13, const float* s13,
+                                      const void* w2, const float* s2, void* out, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!experts_ptrs_ok(x, ids, weights, w13, s13, w2, s2, out), MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!experts_aligned(x, w13, w2, out), MOE_ERR_ALIGNMENT);
+  const ExpertsWs w = carve_experts(workspace, T, H, I, E, k);
+  MOE_RETURN_IF(!workspace || workspace_bytes < w.total, MOE_ERR_WORKSPACE);
+  return launch_experts(x, ids, id_bytes, weights, T, H, I, E, k, w13, s13, w2, s2, out, w, (hipStream_t)stream);
+}
+
+namespace {
+struct BlockWs {
+  void* route_ws;
+  size_t route_bytes;
+  uint16_t* logits;
+  int32_t* ids;
+  uint16_t* weights;
+  void* experts_ws;
+  size_t experts_bytes;
+  size_t total;
+};
+
+BlockWs carve_block(void* base, int T, int H, int I, int E, int k) {
+  BlockWs b{};
+  WsCarver c(base);
+  b.route_bytes = moe_mi355x_route_workspace_bytes(T, H, E);
+  b.route_ws = c.take<char>(b.route_bytes);
+  b.logits = c.take<uint16_t>((size_t)T * E);
+  b.ids = c.take<int32_t>((size_t)T * k);
+  b.weights = c.take<uint16_t>((size_t)T * k);
+  b.experts_bytes = carve_experts(nullptr, T, H, I, E, k).total;
+  b.experts_ws = c.take<char>(b.experts_bytes);
+  b.total = moe_align_up(c.off, 256);
+  return b;
+}
+}  // namespace
+
+extern "C" size_t moe_mi355x_block_workspace_bytes(int T, int H, int I, int E, int k) {
+  if (!experts_args_ok(T, H, I, E, k, 4)) return 0;
+  return carve_block(nullptr, T, H, I, E, k).total;
+}
+
+extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                                    int renorm, const void* w13, const float* s13, const void* w2,
+                                    const float* s2, void* out, void* logits, void* ids, int id_bytes,
+                                    void* weights, void* workspace, size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!x || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!experts_aligned(x, w13, w2, out) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
+  const BlockWs b = carve_block(workspace, T, H, I, E, k);
+  MOE_RETURN_IF(!workspace || workspace_bytes < b.total, MOE_ERR_WORKSPACE);
+  hipStream_t s = (hipStream_t)stream;
+  void* lg = logits ? logits : (void*)b.logits;
+  void* id_out = ids ? ids : (void*)b.ids;
+  const int idb = ids ? id_bytes : 4;
+  void* wt = weights ? weights : (void*)b.weights;
+  int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s);
+  if (rc) return rc;
+  const ExpertsWs w = carve_experts(b.experts_ws, T, H, I, E, k);
+  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s);
+}

@@ -1,0 +1,210 @@
+// Router: bf16 logits GEMM on MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation),
+// then a one-wave-per-token softmax / top-k / renormalise pass.
+//
+// Reference: Qwen3MoeTopKRouter.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267.
+#include "common.h"
+
+namespace {
+
+constexpr int kRouterTileT = 16;    // tokens per MFMA tile
+constexpr int kRouterWaveE = 16;    // experts per wave
+constexpr int kRouterBlockE = 64;   // experts per workgroup (4 waves)
+
+// partial[z, t, e] = sum over k in chunk z of x[t, k] * w[e, k]   (fp32)
+// grid (ceil(T/16), ceil(E/64), ksplit), block 256.
+__global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wr, int T, int H,
+                                                          int E, int kchunk, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * kRouterTileT;
+  const int e0 = blockIdx.y * kRouterBlockE + wave * kRouterWaveE;
+  if (e0 >= E) return;  // wave-uniform
+  const int rt = min(t0 + (lane & 15), T - 1);  // clamped rows compute garbage that is never stored
+  const int re = min(e0 + (lane & 15), E - 1);
+  const int kq = (lane >> 4) * 8;
+  const int kbeg = blockIdx.z * kchunk;
+  const int kend = min(H, kbeg + kchunk);
+  const uint16_t* xa = x + (long)rt * H + kq;
+  const uint16_t* wb = wr + (long)re * H + kq;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  int k = kbeg;
+  for (; k + 128 <= kend; k += 128) {
+    v8bf a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      a[u] = *(const v8bf*)(xa + k + 32 * u);
+      b[u] = *(const v8bf*)(wb + k + 32 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[u], acc, 0, 0, 0);
+  }
+  for (; k < kend; k += 32) {
+    v8bf a = *(const v8bf*)(xa + k), b = *(const v8bf*)(wb + k);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  // D[i][j] lives in lane j + 16*(i/4), element i%4; i = token, j = expert.
+  const int e = e0 + (lane & 15);
+  if (e >= E) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * (lane >> 4) + r;
+    if (t < T) part[((long)blockIdx.z * T + t) * E + e] = acc[r];
+  }
+}
+
+// bf16 bit pattern -> unsigned key that orders like the value (-0 folded onto +0).
+__device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
+  if (b == 0x8000u) b = 0;
+  return (b & 0x8000u) ? (uint32_t)(~b & 0xffffu) : (uint32_t)(b | 0x8000u);
+}
+
+// One wave per token.  Each lane holds experts lane, lane+64, lane+128, lane+192.
+// Either sums router partials (part != nullptr) and writes bf16 logits, or reads logits.
+__global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ part, int ksplit,
+                                                           const uint16_t* __restrict__ logits_in, int T,
+                                                           int E, int k, int renorm,
+                                                           uint16_t* __restrict__ logits_out, void* ids,
+                                                           int id_bytes, uint16_t* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  uint16_t lb[4];
+  bool valid[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int e = lane + 64 * c;
+    valid[c] = e < E;
+    lb[c] = 0;
+    if (!valid[c]) continue;
+    if (part) {
+      float s = 0.f;
+      for (int z = 0; z < ksplit; ++z) s += part[((long)z * T + t) * E + e];
+      lb[c] = f32_to_bf16(s);
+      if (logits_out) logits_out[(long)t * E + e] = lb[c];
+    } else {
+      lb[c] = logits_in[(long)t * E + e];
+    }
+  }
+  // softmax in fp32 (modeling_qwen3_moe.py:261)
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (valid[c]) m = fmaxf(m, bf16_to_f32(lb[c]));
+  m = wave_max(m);
+  float ex[4];
+  float zsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    ex[c] = valid[c] ? expf(bf16_to_f32(lb[c]) - m) : 0.f;
+    zsum += ex[c];
+  }
+  zsum = wave_sum(zsum);
+  uint32_t key[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    key[c] = valid[c] ? ((bf16_order_key(lb[c]) << 16) | (0xffffu - (uint32_t)(lane + 64 * c))) : 0u;
+  // top-k: k rounds of wave arg-max on (logit, -id)   (modeling_qwen3_moe.py:262)
+  int my_e = 0;
+  float my_p = 0.f, psum = 0.f;
+  for (int j = 0; j < k; ++j) {
+    uint32_t best = key[0];
+#pragma unroll
+    for (int c = 1; c < 4; ++c) best = key[c] > best ? key[c] : best;
+    best = wave_max_u32(best);
+    const int ew = (int)(0xffffu - (best & 0xffffu));
+    const int owner = ew & 63, slot = ew >> 6;
+    float pv = 0.f;
+    if (lane == owner) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (c == slot) {
+          pv = ex[c] / zsum;
+          key[c] = 0u;
+        }
+    }
+    pv = __shfl(pv, owner, MOE_WAVE);
+    psum += pv;  // sequential fp32 sum in top-k order, identical in every lane
+    if (lane == j) {
+      my_e = ew;
+      my_p = pv;
+    }
+  }
+  if (lane < k) {
+    const float wv = renorm ? my_p / psum : my_p;  // modeling_qwen3_moe.py:263-266
+    weights[(long)t * k + lane] = f32_to_bf16(wv);
+    if (id_bytes == 8)
+      ((int64_t*)ids)[(long)t * k + lane] = my_e;
+    else
+      ((int32_t*)ids)[(long)t * k + lane] = my_e;
+  }
+}
+
+int route_ksplit(int T, int H, int E) {
+  const int tiles = ((T + kRouterTileT - 1) / kRouterTileT) * ((E + kRouterBlockE - 1) / kRouterBlockE);
+  int ks = (256 + tiles - 1) / tiles;
+  const int kmax = H / 256 > 0 ? H / 256 : 1;
+  if (ks > kmax) ks = kmax;
+  if (ks < 1) ks = 1;
+  return ks;
+}
+
+int route_kchunk(int H, int ks) {
+  int c = (H + ks - 1) / ks;
+  return (c + 31) / 32 * 32;
+}
+
+bool route_args_ok(int T, int H, int E, int k, int id_bytes) {
+  return T >= 0 && H > 0 && H % 32 == 0 && E >= 1 && E <= 256 && k >= 1 && k <= 32 && k <= E &&
+         (id_bytes == 4 || id_bytes == 8);
+}
+
+}  // namespace
+
+extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E) {
+  if (T <= 0 || H <= 0 || E <= 0) return 0;
+  const int ks = route_ksplit(T, H, E);
+  return moe_align_up((size_t)ks * T * E * sizeof(float), 256);
+}
+
+int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                     void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                     size_t workspace_bytes, hipStream_t s) {
+  if (T == 0) return MOE_OK;
+  const int ks = route_ksplit(T, H, E);
+  const int kchunk = route_kchunk(H, ks);
+  const int ks_eff = (H + kchunk - 1) / kchunk;
+  MOE_RETURN_IF(workspace_bytes < moe_mi355x_route_workspace_bytes(T, H, E) || !workspace, MOE_ERR_WORKSPACE);
+  float* part = (float*)workspace;
+  dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
+  hipLaunchKernelGGL(router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+                     (const uint16_t*)w_router, T, H, E, kchunk, part);
+  MOE_CHECK_LAUNCH();
+  hipLaunchKernelGGL(topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
+                     (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes,
+                     (uint16_t*)weights);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+extern "C" int moe_mi355x_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                                void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!route_args_ok(T, H, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!x || !w_router || !ids || !weights, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!moe_aligned16(x) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
+  return moe_launch_route(x, w_router, T, H, E, k, renorm, logits, ids, id_bytes, weights, workspace,
+                          workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, int renorm, void* ids,
+                                       int id_bytes, void* weights, void* stream) {
+  MOE_RETURN_IF(!route_args_ok(T, 32, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!logits || !ids || !weights, MOE_ERR_INVALID_ARG);
+  hipLaunchKernelGGL(topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     (const float*)nullptr, 0, (const uint16_t*)logits, T, E, k, renorm,
+                     (uint16_t*)nullptr, ids, id_bytes, (uint16_t*)weights);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}

@@ -1,0 +1,178 @@
+"""Drop-in MoE modules for the reference server's model path.
+
+The reference backend loads a Hugging Face model (src/inference_server/backends/
+torch_backend.py:38-40); for a Qwen3-MoE checkpoint each decoder layer calls
+``self.mlp(hidden_states)`` (TF/models/qwen3_moe/modeling_qwen3_moe.py:346), a
+``Qwen3MoeSparseMoeBlock``.  Two hook points keep that call signature unchanged:
+
+* ``mi355x_fp8_experts_forward`` has the experts-plugin signature
+  ``forward(self, hidden_states[T,H], top_k_index[T,k], top_k_weights[T,k]) -> [T,H]``
+  (TF/integrations/moe.py:377-382) and is registered in transformers'
+  ``FP8ExpertsInterface`` (TF/integrations/finegrained_fp8.py:757-768) under the key
+  ``"mi355x"``; a model loaded with ``experts_implementation="mi355x"`` dispatches
+  its ``FP8Experts`` modules to it (moe.py:567-570).
+* ``MI355XSparseMoeBlock`` replaces a whole ``Qwen3MoeSparseMoeBlock``
+  (modeling_qwen3_moe.py:270-281) with ``forward(hidden_states[B,S,H]) -> [B,S,H]``;
+  ``swap_moe_blocks(model)`` does it for every layer after ``load_model``.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import kernels
+
+IMPLEMENTATION_KEY = "mi355x"
+
+
+def mi355x_fp8_experts_forward(self: nn.Module, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                               top_k_weights: torch.Tensor) -> torch.Tensor:
+    """Experts forward over ``FP8Experts`` parameters (finegrained_fp8.py:592-680).
+
+    Reads ``gate_up_proj`` e4m3 [E,2I,H], ``gate_up_proj_scale_inv`` fp32 [E,2I/128,H/128],
+    ``down_proj`` e4m3 [E,H,I], ``down_proj_scale_inv`` fp32 [E,H/128,I/128].  Raises like
+    ``fp8_grouped_mm_experts_forward`` (finegrained_fp8.py:504-508) for static activation scales.
+    """
+    if getattr(self, "activation_scheme", "dynamic") == "static":
+        raise NotImplementedError(
+            "the mi355x experts implementation does not support activation_scheme='static'; "
+            "use activation_scheme='dynamic'"
+        )
+    if not getattr(self, "has_gate", True):
+        raise NotImplementedError("the mi355x experts implementation requires gated (gate_up) experts")
+    if getattr(self, "has_bias", False):
+        raise NotImplementedError("the mi355x experts implementation does not support expert biases")
+    if getattr(self, "is_transposed", False):
+        raise NotImplementedError("the mi355x experts implementation expects [E, N, K] (non-transposed) weights")
+    block = getattr(self, "block_size", (128, 128))
+    if block is not None and tuple(block) != (128, 128):
+        raise NotImplementedError(f"block_size must be (128, 128), got {tuple(block)}")
+    if (getattr(self, "swiglu_alpha", None) is not None or getattr(self, "limit", None) is not None):
+        raise NotImplementedError("clamped SwiGLU variants are not supported")
+    out_dtype = hidden_states.dtype
+    x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
+    w = top_k_weights if top_k_weights.dtype == torch.bfloat16 else top_k_weights.to(torch.bfloat16)
+    out = kernels.experts_fp8(x.contiguous(), top_k_index.contiguous(), w.contiguous(), self.gate_up_proj,
+                              self.gate_up_proj_scale_inv, self.down_proj, self.down_proj_scale_inv)
+    return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
+
+
+def register(key: str = IMPLEMENTATION_KEY) -> bool:
+    """Register the experts forward with transformers' FP8 experts interface.
+
+    Returns False when transformers is not importable (the modules below still work).
+    """
+    try:
+        from transformers.integrations.finegrained_fp8 import FP8ExpertsInterface
+    except Exception:  # transformers absent or too old
+        return False
+    FP8ExpertsInterface.register(key, mi355x_fp8_experts_forward)
+    return True
+
+
+class MI355XFp8Experts(nn.Module):
+    """FP8 experts with the ``FP8Experts`` parameter names and layout (finegrained_fp8.py:592-680)."""
+
+    def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int, device=None):
+        super().__init__()
+        self.num_experts = num_experts
+        self.hidden_dim = hidden_dim
+        self.intermediate_dim = intermediate_dim
+        self.block_size = (128, 128)
+        self.activation_scheme = "dynamic"
+        self.has_gate, self.has_bias, self.is_transposed = True, False, False
+        E, H, I = num_experts, hidden_dim, intermediate_dim
+        f8 = torch.float8_e4m3fn
+        self.gate_up_proj = nn.Parameter(torch.empty(E, 2 * I, H, dtype=f8, device=device), requires_grad=False)
+        self.gate_up_proj_scale_inv = nn.Parameter(
+            torch.ones(E, 2 * I // 128, H // 128, dtype=torch.float32, device=device), requires_grad=False)
+        self.down_proj = nn.Parameter(torch.empty(E, H, I, dtype=f8, device=device), requires_grad=False)
+        self.down_proj_scale_inv = nn.Parameter(
+            torch.ones(E, H // 128, I // 128, dtype=torch.float32, device=device), requires_grad=False)
+
+    @classmethod
+    def from_bf16(cls, gate_up_proj: torch.Tensor, down_proj: torch.Tensor) -> "MI355XFp8Experts":
+        """Quantise bf16/fp32 expert weights [E,2I,H] and [E,H,I] with the GPU block quantiser."""
+        E, I2, H = gate_up_proj.shape
+        mod = cls(E, H, I2 // 2, device=gate_up_proj.device)
+        q13, s13 = kernels.quantize_weight_fp8(gate_up_proj.contiguous())
+        q2, s2 = kernels.quantize_weight_fp8(down_proj.contiguous())
+        with torch.no_grad():
+            mod.gate_up_proj.copy_(q13)
+            mod.gate_up_proj_scale_inv.copy_(s13)
+            mod.down_proj.copy_(q2)
+            mod.down_proj_scale_inv.copy_(s2)
+        return mod
+
+    def forward(self, hidden_states, top_k_index, top_k_weights):
+        return mi355x_fp8_experts_forward(self, hidden_states, top_k_index, top_k_weights)
+
+
+class MI355XTopKRouter(nn.Module):
+    """``Qwen3MoeTopKRouter`` (modeling_qwen3_moe.py:249-267): returns (logits, scores, indices)."""
+
+    def __init__(self, num_experts: int, hidden_dim: int, top_k: int, norm_topk_prob: bool = True, device=None):
+        super().__init__()
+        self.top_k = top_k
+        self.num_experts = num_experts
+        self.norm_topk_prob = norm_topk_prob
+        self.hidden_dim = hidden_dim
+        self.weight = nn.Parameter(torch.zeros(num_experts, hidden_dim, dtype=torch.bfloat16, device=device),
+                                   requires_grad=False)
+
+    def forward(self, hidden_states):
+        x = hidden_states.reshape(-1, self.hidden_dim)
+        return kernels.route(x.contiguous(), self.weight, self.top_k, self.norm_topk_prob)
+
+
+class MI355XSparseMoeBlock(nn.Module):
+    """Drop-in ``Qwen3MoeSparseMoeBlock``: ``forward(hidden_states[B,S,H]) -> [B,S,H]`` (bf16)."""
+
+    def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int, top_k: int,
+                 norm_topk_prob: bool = True, device=None):
+        super().__init__()
+        self.gate = MI355XTopKRouter(num_experts, hidden_dim, top_k, norm_topk_prob, device=device)
+        self.experts = MI355XFp8Experts(num_experts, hidden_dim, intermediate_dim, device=device)
+
+    @classmethod
+    def from_hf_block(cls, block: nn.Module, norm_topk_prob: bool | None = None) -> "MI355XSparseMoeBlock":
+        """Build from a ``Qwen3MoeSparseMoeBlock`` with bf16 experts (quantised here, 128x128 blocks)
+        or from one whose experts already carry ``FP8Experts`` parameters."""
+        gate, experts = block.gate, block.experts
+        E, H = gate.weight.shape
+        renorm = gate.norm_topk_prob if norm_topk_prob is None else norm_topk_prob
+        dev = gate.weight.device
+        if experts.gate_up_proj.dtype == torch.float8_e4m3fn:
+            I = experts.gate_up_proj.shape[1] // 2
+            new = cls(E, H, I, gate.top_k, renorm, device=dev)
+            with torch.no_grad():
+                for name in ("gate_up_proj", "gate_up_proj_scale_inv", "down_proj", "down_proj_scale_inv"):
+                    getattr(new.experts, name).copy_(getattr(experts, name))
+        else:
+            I = experts.gate_up_proj.shape[1] // 2
+            new = cls(E, H, I, gate.top_k, renorm, device=dev)
+            new.experts = MI355XFp8Experts.from_bf16(experts.gate_up_proj.detach(), experts.down_proj.detach())
+        with torch.no_grad():
+            new.gate.weight.copy_(gate.weight.to(torch.bfloat16))
+        return new
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        e = self.experts
+        return kernels.moe_block_fp8(hidden_states.contiguous(), self.gate.weight, self.gate.top_k, e.gate_up_proj,
+                                     e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv,
+                                     norm_topk_prob=self.gate.norm_topk_prob)
+
+
+def swap_moe_blocks(model: nn.Module) -> int:
+    """Replace every Qwen3-MoE sparse block of ``model`` by ``MI355XSparseMoeBlock``; returns the count.
+
+    Intended right after the reference's ``TorchBackend.load_model`` (torch_backend.py:33-53).
+    """
+    targets = [(name, mod) for name, mod in model.named_modules()
+               if type(mod).__name__ == "Qwen3MoeSparseMoeBlock"]
+    for name, mod in targets:
+        parent_name, _, child = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, child, MI355XSparseMoeBlock.from_hf_block(mod))
+    return len(targets)

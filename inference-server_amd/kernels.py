@@ -1,0 +1,259 @@
+"""torch-facing wrappers of the C-ABI entry points.
+
+torch supplies device memory and the current HIP stream; every computation runs in
+the HIP kernels of ``libmoe_mi355x.so``.  Tensors must live on a ROCm device, be
+contiguous and carry the dtypes listed per op; violations raise ``ValueError`` /
+``TypeError`` before anything is launched.  Workspaces are fresh ``torch.empty``
+buffers from the caching allocator, so calls on different streams never share one.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+FP8 = torch.float8_e4m3fn
+BLOCK = 128
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
+    if not isinstance(dtypes, (tuple, list)):
+        dtypes = (dtypes,)
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} must have dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _id_bytes(ids: torch.Tensor) -> int:
+    if ids.dtype == torch.int64:
+        return 8
+    if ids.dtype == torch.int32:
+        return 4
+    raise TypeError(f"expert ids must be int32 or int64, got {ids.dtype}")
+
+
+# ---------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------
+
+
+def route(hidden_states: torch.Tensor, router_weight: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
+          index_dtype: torch.dtype = torch.int64):
+    """``Qwen3MoeTopKRouter.forward`` (TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267).
+
+    Returns ``(router_logits bf16 [T,E], router_scores bf16 [T,k], router_indices [T,k])``,
+    the reference's return order.  Ties are broken towards the lower expert id.
+    """
+    _need(router_weight, "router_weight", torch.bfloat16, 2)
+    E, H = router_weight.shape
+    x = hidden_states.reshape(-1, H)
+    _need(x, "hidden_states", torch.bfloat16, 2)
+    if x.device != router_weight.device:
+        raise ValueError("hidden_states and router_weight must be on the same device")
+    if not 1 <= top_k <= min(E, 32):
+        raise ValueError(f"top_k must be in [1, min(E, 32)], got {top_k}")
+    T = x.shape[0]
+    lib = _lib.load()
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
+    ids = torch.empty((T, top_k), dtype=index_dtype, device=x.device)
+    w = torch.empty((T, top_k), dtype=torch.bfloat16, device=x.device)
+    ws = _ws(lib.moe_mi355x_route_workspace_bytes(T, H, E), x.device)
+    _lib.check(lib.moe_mi355x_route(x.data_ptr(), router_weight.data_ptr(), T, H, E, top_k, int(norm_topk_prob),
+                                    logits.data_ptr(), ids.data_ptr(), _id_bytes(ids), w.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), _stream(x)), "moe_mi355x_route")
+    return logits, w, ids
+
+
+def topk_softmax(router_logits: torch.Tensor, top_k: int, norm_topk_prob: bool = True,
+                 index_dtype: torch.dtype = torch.int64):
+    """softmax(fp32) -> top-k -> renormalise -> bf16 (modeling_qwen3_moe.py:261-266).
+
+    Returns ``(router_scores bf16 [T,k], router_indices [T,k])``.
+    """
+    _need(router_logits, "router_logits", torch.bfloat16, 2)
+    T, E = router_logits.shape
+    if not 1 <= top_k <= min(E, 32):
+        raise ValueError(f"top_k must be in [1, min(E, 32)], got {top_k}")
+    ids = torch.empty((T, top_k), dtype=index_dtype, device=router_logits.device)
+    w = torch.empty((T, top_k), dtype=torch.bfloat16, device=router_logits.device)
+    lib = _lib.load()
+    _lib.check(lib.moe_mi355x_topk_softmax(router_logits.data_ptr(), T, E, top_k, int(norm_topk_prob),
+                                           ids.data_ptr(), _id_bytes(ids), w.data_ptr(), _stream(router_logits)),
+               "moe_mi355x_topk_softmax")
+    return w, ids
+
+
+# ---------------------------------------------------------------------------
+# sort / align
+# ---------------------------------------------------------------------------
+
+
+def align(top_k_index: torch.Tensor, num_experts: int, block_m: int = 16) -> dict:
+    """Stable expert sort, counts, offsets and tile list (TF/integrations/moe.py:389-403).
+
+    Returns a dict with ``perm`` int32 [S], ``counts`` int32 [E], ``offsets`` int32 [E+1]
+    (exclusive), ``tiles`` int32 [max_tiles, 4] and ``n_tiles`` int32 [1].
+    """
+    _need(top_k_index, "top_k_index", (torch.int32, torch.int64))
+    if top_k_index.dim() != 2:
+        raise ValueError("top_k_index must be [T, k]")
+    T, k = top_k_index.shape
+    if not 1 <= num_experts <= 256:
+        raise ValueError("num_experts must be in [1, 256]")
+    S = T * k
+    lib = _lib.load()
+    dev = top_k_index.device
+    max_tiles = max(lib.moe_mi355x_align_max_tiles(S, num_experts, block_m), 1)
+    out = {
+        "perm": torch.empty(S, dtype=torch.int32, device=dev),
+        "counts": torch.empty(num_experts, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        "tiles": torch.empty((max_tiles, 4), dtype=torch.int32, device=dev),
+        "n_tiles": torch.empty(1, dtype=torch.int32, device=dev),
+    }
+    ws = _ws(lib.moe_mi355x_align_workspace_bytes(S, num_experts), dev)
+    _lib.check(lib.moe_mi355x_align(top_k_index.data_ptr(), _id_bytes(top_k_index), T, k, num_experts, block_m,
+                                    out["perm"].data_ptr(), out["counts"].data_ptr(), out["offsets"].data_ptr(),
+                                    out["tiles"].data_ptr(), out["n_tiles"].data_ptr(), ws.data_ptr(), ws.numel(),
+                                    _stream(top_k_index)), "moe_mi355x_align")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# quantisation
+# ---------------------------------------------------------------------------
+
+
+def quantize_act_fp8(x: torch.Tensor):
+    """Per-row, per-128-column dynamic e4m3 quantisation. Returns (q fp8 [R,C], scales fp32 [R,C/128])."""
+    _need(x, "x", torch.bfloat16, 2)
+    R, C = x.shape
+    if C % BLOCK:
+        raise ValueError(f"columns must be a multiple of {BLOCK}")
+    q = torch.empty((R, C), dtype=FP8, device=x.device)
+    s = torch.empty((R, C // BLOCK), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().moe_mi355x_quantize_act_fp8(x.data_ptr(), R, C, q.data_ptr(), s.data_ptr(),
+                                                       _stream(x)), "moe_mi355x_quantize_act_fp8")
+    return q, s
+
+
+def quantize_weight_fp8(w: torch.Tensor):
+    """128x128 block weight quantisation, ``Fp8Quantize._quantize_one``
+    (TF/integrations/finegrained_fp8.py:903-941).  w: [..., N, K] bf16 or fp32.
+    Returns (q fp8 [..., N, K], scale_inv fp32 [..., N/128, K/128])."""
+    _need(w, "w", (torch.bfloat16, torch.float32))
+    if w.dim() < 2:
+        raise ValueError("w must be at least 2-D")
+    *lead, N, K = w.shape
+    if N % BLOCK or K % BLOCK:
+        raise ValueError(f"weight dims must be multiples of {BLOCK}")
+    B = 1
+    for d in lead:
+        B *= d
+    q = torch.empty(w.shape, dtype=FP8, device=w.device)
+    s = torch.empty((*lead, N // BLOCK, K // BLOCK), dtype=torch.float32, device=w.device)
+    _lib.check(_lib.load().moe_mi355x_quantize_weight_fp8(w.data_ptr(), 0 if w.dtype == torch.bfloat16 else 1,
+                                                          B, N, K, q.data_ptr(), s.data_ptr(), _stream(w)),
+               "moe_mi355x_quantize_weight_fp8")
+    return q, s
+
+
+# ---------------------------------------------------------------------------
+# experts / block
+# ---------------------------------------------------------------------------
+
+
+def _check_expert_weights(w13, s13, w2, s2):
+    _need(w13, "gate_up_proj", FP8, 3)
+    _need(w2, "down_proj", FP8, 3)
+    _need(s13, "gate_up_proj_scale_inv", torch.float32, 3)
+    _need(s2, "down_proj_scale_inv", torch.float32, 3)
+    E, I2, H = w13.shape
+    I = I2 // 2
+    if I2 % 2 or I % BLOCK or H % BLOCK:
+        raise ValueError(f"gate_up_proj must be [E, 2I, H] with I, H multiples of {BLOCK}")
+    if tuple(w2.shape) != (E, H, I):
+        raise ValueError(f"down_proj must be [E, H, I] = {(E, H, I)}, got {tuple(w2.shape)}")
+    if tuple(s13.shape) != (E, I2 // BLOCK, H // BLOCK) or tuple(s2.shape) != (E, H // BLOCK, I // BLOCK):
+        raise ValueError("scale_inv tensors must be [E, N/128, K/128] (128x128 blocks)")
+    if H > 4096 or I > 4096 or not 1 <= E <= 256:
+        raise ValueError("supported shapes: H, I <= 4096 and 1 <= E <= 256")
+    return E, H, I
+
+
+def experts_fp8(hidden_states, top_k_index, top_k_weights, gate_up_proj, gate_up_proj_scale_inv, down_proj,
+                down_proj_scale_inv):
+    """FP8 block-scaled experts, ``fp8_grouped_mm_experts_forward``
+    (TF/integrations/finegrained_fp8.py:498-589).  Returns bf16 [T, H]."""
+    E, H, I = _check_expert_weights(gate_up_proj, gate_up_proj_scale_inv, down_proj, down_proj_scale_inv)
+    _need(hidden_states, "hidden_states", torch.bfloat16, 2)
+    _need(top_k_index, "top_k_index", (torch.int32, torch.int64), 2)
+    _need(top_k_weights, "top_k_weights", torch.bfloat16, 2)
+    T = hidden_states.shape[0]
+    if hidden_states.shape[1] != H:
+        raise ValueError(f"hidden_states must be [T, {H}]")
+    if top_k_index.shape[0] != T or tuple(top_k_weights.shape) != tuple(top_k_index.shape):
+        raise ValueError("top_k_index and top_k_weights must both be [T, k]")
+    k = top_k_index.shape[1]
+    if not 1 <= k <= min(E, 32):
+        raise ValueError("k must be in [1, min(E, 32)]")
+    lib = _lib.load()
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden_states.device)
+    ws = _ws(lib.moe_mi355x_experts_workspace_bytes(T, H, I, E, k), hidden_states.device)
+    _lib.check(lib.moe_mi355x_experts_fp8(hidden_states.data_ptr(), top_k_index.data_ptr(), _id_bytes(top_k_index),
+                                          top_k_weights.data_ptr(), T, H, I, E, k, gate_up_proj.data_ptr(),
+                                          gate_up_proj_scale_inv.data_ptr(), down_proj.data_ptr(),
+                                          down_proj_scale_inv.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          _stream(hidden_states)), "moe_mi355x_experts_fp8")
+    return out
+
+
+def moe_block_fp8(hidden_states, router_weight, top_k, gate_up_proj, gate_up_proj_scale_inv, down_proj,
+                  down_proj_scale_inv, norm_topk_prob=True, return_routing=False, index_dtype=torch.int64):
+    """Router + FP8 experts in one call (``Qwen3MoeSparseMoeBlock.forward``,
+    TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281).  hidden_states: [..., H] bf16."""
+    E, H, I = _check_expert_weights(gate_up_proj, gate_up_proj_scale_inv, down_proj, down_proj_scale_inv)
+    _need(router_weight, "router_weight", torch.bfloat16, 2)
+    if tuple(router_weight.shape) != (E, H):
+        raise ValueError(f"router_weight must be [{E}, {H}]")
+    shape = hidden_states.shape
+    x = hidden_states.reshape(-1, H)
+    _need(x, "hidden_states", torch.bfloat16, 2)
+    if not 1 <= top_k <= min(E, 32):
+        raise ValueError("top_k must be in [1, min(E, 32)]")
+    T = x.shape[0]
+    lib = _lib.load()
+    dev = x.device
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    logits = ids = w = None
+    if return_routing:
+        logits = torch.empty((T, E), dtype=torch.bfloat16, device=dev)
+        ids = torch.empty((T, top_k), dtype=index_dtype, device=dev)
+        w = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+    ws = _ws(lib.moe_mi355x_block_workspace_bytes(T, H, I, E, top_k), dev)
+    _lib.check(lib.moe_mi355x_block_fp8(
+        x.data_ptr(), router_weight.data_ptr(), T, H, I, E, top_k, int(norm_topk_prob), gate_up_proj.data_ptr(),
+        gate_up_proj_scale_inv.data_ptr(), down_proj.data_ptr(), down_proj_scale_inv.data_ptr(), out.data_ptr(),
+        logits.data_ptr() if logits is not None else None, ids.data_ptr() if ids is not None else None,
+        _id_bytes(ids) if ids is not None else 4, w.data_ptr() if w is not None else None,
+        ws.data_ptr(), ws.numel(), _stream(x)), "moe_mi355x_block_fp8")
+    out = out.reshape(shape)
+    if return_routing:
+        return out, (logits, w, ids)
+    return out
