@@ -1,0 +1,280 @@
+"""Benchmark of the MI355X Qwen3-MoE FP8 expert layer (one GPU).
+
+One step = one MoE block forward (router + FP8 experts) of the Qwen3-30B-A3B-shaped layer
+(hidden 2048, 128 experts, top-8, moe_intermediate 768, 128x128 block scales) over one
+batch of synthetic tokens already resident in HBM.  The headline line is the decode batch
+of 64 tokens; a sweep over the other decode batches and the 4096-token
+Zipf-skewed prefill chunk (config 3) rides along in ``sweep``.
+
+Weights are rotated over enough copies that one step's weights never sit in the 256 MB
+last-level cache from an earlier step; inputs rotate too, so routing changes every step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--no-sweep] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "MoE layer µs + % roofline (HBM GB/s / FP8 MFMA), Qwen3-30B-A3B shape, bs 1–4096"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+LLC_BYTES = 256 * 2 ** 20
+
+E, H, I, K_TOP = 128, 2048, 768, 8
+
+
+def expert_bytes(H, I):
+    """Weight + scale bytes of one expert (gate_up and down), 4,719,744 B for the 30B shape."""
+    return 2 * I * H + H * I + 4 * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128))
+
+
+def gate_up_bytes(n_active, T, H, I, k):
+    """Algorithmic HBM bytes of one gate_up launch: active experts' W13 + scales, the fp8
+    activations and their scales read, the bf16 intermediate written."""
+    return (n_active * (2 * I * H + 4 * (2 * I // 128) * (H // 128)) + T * H + 4 * T * (H // 128)
+            + 2 * T * k * I)
+
+
+def gate_up_flops(T, H, I, k):
+    return 2.0 * T * k * (2 * I) * H
+
+
+def layer_bytes(n_active, T, H, I, E):
+    return n_active * expert_bytes(H, I) + 2 * E * H + 4 * T * H
+
+
+def layer_flops(T, H, I, E, k):
+    return T * k * (2.0 * H * 2 * I + 2.0 * I * H) + 2.0 * T * H * E
+
+
+class Layer:
+    def __init__(self, pkg, torch, dev, n_copies):
+        g = torch.Generator(device=dev).manual_seed(0)
+        self.wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        w13 = (torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q13, s13 = pkg.quantize_weight_fp8(w13)
+        q2, s2 = pkg.quantize_weight_fp8(w2)
+        del w13, w2
+        self.copies = [(q13, s13, q2, s2)] + [tuple(t.clone() for t in (q13, s13, q2, s2))
+                                             for _ in range(n_copies - 1)]
+
+
+def make_inputs(torch, dev, T, n, zipf_beta=None):
+    g = torch.Generator(device=dev).manual_seed(1000 + T)
+    xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    if zipf_beta is not None:
+        for x in xs:  # hidden dim 0 carries a constant 1, router column 0 the Zipf bias
+            x[:, 0] = 1.0
+    return xs
+
+
+def zipf_router(torch, wr, beta):
+    import numpy as np
+
+    r = np.random.default_rng(0).permutation(E) + 1
+    b = torch.tensor(beta * (-1.1 * np.log(r)), dtype=torch.float32, device=wr.device)
+    w = wr.clone()
+    w[:, 0] = b.to(torch.bfloat16)
+    return w
+
+
+def calibrate_zipf(pkg, torch, dev, wr, T=4096):
+    """Bisect beta so that the 10 most loaded experts take 50% of the T*k assignments."""
+    x = make_inputs(torch, dev, T, 1, zipf_beta=0.0)[0]
+    lo, hi = 0.0, 8.0
+    share = 0.0
+    for _ in range(24):
+        mid = 0.5 * (lo + hi)
+        _, _, ids = pkg.route(x, zipf_router(torch, wr, mid), K_TOP)
+        cnt = torch.bincount(ids.reshape(-1), minlength=E).sort(descending=True).values
+        share = float(cnt[:10].sum()) / (T * K_TOP)
+        if share < 0.5:
+            lo = mid
+        else:
+            hi = mid
+    return 0.5 * (lo + hi), share
+
+
+def run_config(pkg, torch, layer, T, steps, warmup, router, xs, profile_slots=True):
+    """Times `steps` block forwards; returns (ms_per_step, per-slot avg ms, mean active experts)."""
+    lib = pkg._lib.load()
+    expected_active = E * (1.0 - (1.0 - K_TOP / E) ** T)
+    per_step = layer_bytes(expected_active, T, H, I, E)
+    n_rot = max(2, min(len(layer.copies), math.ceil(2 * LLC_BYTES / max(1.0, per_step))))
+
+    def step(i, routing=False):
+        q13, s13, q2, s2 = layer.copies[i % n_rot]
+        return pkg.moe_block_fp8(xs[i % len(xs)], router, K_TOP, q13, s13, q2, s2, return_routing=routing)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(steps):
+        step(i)
+    en.record()
+    torch.cuda.synchronize()
+    ms = st.elapsed_time(en) / steps
+
+    slots = {}
+    active = []
+    if profile_slots:
+        import ctypes
+
+        lib.moe_mi355x_profile_enable(1)
+        ids_seen = []
+        for i in range(steps):
+            _, (_, _, ids) = step(i, routing=True)
+            ids_seen.append(ids)
+        torch.cuda.synchronize()
+        for slot in range(8):
+            n, tot = ctypes.c_int(0), ctypes.c_double(0.0)
+            pkg._lib.check(lib.moe_mi355x_profile_read(slot, ctypes.byref(n), ctypes.byref(tot)), "profile_read")
+            if n.value:
+                slots[lib.moe_mi355x_profile_slot_name(slot).decode()] = tot.value / steps
+        lib.moe_mi355x_profile_enable(0)
+        active = [int(torch.unique(ids).numel()) for ids in ids_seen]
+    n_active = sum(active) / len(active) if active else float("nan")
+    return ms, slots, n_active, n_rot
+
+
+def roofline_for(T, slots, n_active):
+    dom = max(slots, key=slots.get)
+    dur_s = slots[dom] * 1e-3
+    if T >= 1024:  # prefill chunk: the grouped GEMMs are MFMA-bound
+        flops = gate_up_flops(T, H, I, K_TOP)
+        achieved = flops / slots["gemm_gate_up"] / 1e9  # TFLOP/s
+        return {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
+                "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                "traffic": None, "algorithmic_flop": flops, "avg_us": round(slots["gemm_gate_up"] * 1e3, 2),
+                "dominant": dom}
+    byts = gate_up_bytes(n_active, T, H, I, K_TOP)
+    achieved = byts / (slots["gemm_gate_up"] * 1e-3) / 1e9  # GB/s
+    return {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "algorithmic_bytes": int(byts), "avg_us": round(slots["gemm_gate_up"] * 1e3, 2), "dominant": dom,
+            "dominant_us": round(dur_s * 1e6, 2)}
+
+
+def cpu_baseline(pkg, torch, layer, router, x, budget_s=20.0):
+    """The CPU oracle (dequantise-then-fp32-matmul restatement of the reference path), timed
+    on this host on the headline workload; median over as many steps as fit the budget."""
+    import numpy as np
+
+    from oracle import moe_oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    q13, s13, q2, s2 = layer.copies[0]
+    q13n, q2n = q13.view(torch.uint8).cpu().numpy(), q2.view(torch.uint8).cpu().numpy()
+    s13n, s2n = s13.cpu().numpy(), s2.cpu().numpy()
+    xn, wrn = x.float().cpu().numpy(), router.float().cpu().numpy()
+    T = xn.shape[0]
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        lg, ids, w = orc.route(xn, wrn, K_TOP)
+        orc.experts_fp8(xn, ids, w, q13n, s13n, q2n, s2n, acc=np.float32)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s or len(times) >= 10:
+            break
+    med = sorted(times)[len(times) // 2]
+    return {"value": round(T / med, 2), "unit": "tokens/s", "us_per_layer": round(med * 1e6, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"{len(times)} block forwards of the {T}-token decode batch (numpy oracle: router, "
+                      f"per-expert dequantise then fp32 matmul), median"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (expert-parallel sharding "
+              "is a design note); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    pkg._lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    layer = Layer(pkg, torch, dev, n_copies=16)
+    router = layer.wr
+
+    T = args.tokens
+    xs = make_inputs(torch, dev, T, 8)
+    ms, slots, n_active, n_rot = run_config(pkg, torch, layer, T, args.steps, args.warmup, router, xs)
+    line = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_layer": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {"workload": f"qwen3-30b-a3b moe layer, fp8 128x128 block scales, decode batch {T}",
+                   "tokens": T, "hidden": H, "experts": E, "top_k": K_TOP, "moe_intermediate": I,
+                   "routing": "router-driven (x~N(0,1), W_r~N(0,0.02): uniform in distribution)",
+                   "weight_copies_rotated": n_rot, "mean_active_experts": round(n_active, 2)},
+        "roofline": roofline_for(T, slots, n_active),
+        "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()},
+        "layer_hbm_frac": round(layer_bytes(n_active, T, H, I, E) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    if not args.no_sweep:
+        sweep = []
+        beta, share = calibrate_zipf(pkg, torch, dev, router)
+        for Ts in (1, 8, 32, 64, 128, 256, 4096):
+            skew = Ts == 4096
+            xs_s = make_inputs(torch, dev, Ts, 4, zipf_beta=beta if skew else None)
+            r = zipf_router(torch, router, beta) if skew else router
+            steps = 20 if Ts < 4096 else 10
+            ms_s, slots_s, act_s, _ = run_config(pkg, torch, layer, Ts, steps, 5, r, xs_s)
+            rl = roofline_for(Ts, slots_s, act_s)
+            entry = {"tokens": Ts, "us_per_layer": round(ms_s * 1e3, 2), "tokens_per_s": round(Ts / (ms_s * 1e-3), 1),
+                     "mean_active_experts": round(act_s, 2), "roofline": rl,
+                     "kernels_us": {k: round(v * 1e3, 2) for k, v in slots_s.items()}}
+            if skew:
+                entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
+                entry["layer_tflops"] = round(layer_flops(Ts, H, I, E, K_TOP) / (ms_s * 1e-3) / 1e12, 1)
+            else:
+                entry["layer_hbm_frac"] = round(layer_bytes(act_s, Ts, H, I, E) / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            sweep.append(entry)
+            print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
+        line["sweep"] = sweep
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(pkg, torch, layer, router, xs[0])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -126,6 +126,18 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
                          const float* s2, void* out, void* logits, void* ids, int id_bytes,
                          void* weights, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Kernel timing (instrumentation; no counterpart in the reference).  While enabled, each
+ * kernel launch of this library is bracketed by hipEvents on its stream; profile_read
+ * waits for them and returns the launch count and summed duration (ms) of one slot:
+ *   0 router_gemm  1 topk_softmax  2 quant_act  3 align  4 gemm_gate_up  5 quant_h
+ *   6 gemm_down    7 combine
+ * Enabling (or disabling) clears what was recorded.
+ */
+int moe_mi355x_profile_enable(int on);
+int moe_mi355x_profile_read(int slot, int* count, double* total_ms);
+const char* moe_mi355x_profile_slot_name(int slot);
+
 #ifdef __cplusplus
 }
 #endif

@@ -206,7 +206,7 @@ int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, i
                      int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles, void* workspace,
                      size_t workspace_bytes, hipStream_t s) {
   if (S <= kSingleMaxS) {
-    hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(kChunk), 0, s, ids, id_bytes, S, E, block_m, perm,
+    MOE_LAUNCH(MOE_PROF_ALIGN, s, align_single_kernel, dim3(1), dim3(kChunk), 0, s, ids, id_bytes, S, E, block_m, perm,
                        counts, offsets, tiles, n_tiles);
     MOE_CHECK_LAUNCH();
     return MOE_OK;
@@ -214,12 +214,12 @@ int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, i
   MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_align_workspace_bytes(S, E), MOE_ERR_WORKSPACE);
   const int nb = (S + kChunk - 1) / kChunk;
   int32_t* bc = (int32_t*)workspace;
-  hipLaunchKernelGGL(align_count_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E, bc);
+  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_count_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E, bc);
   MOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(kChunk), 0, s, bc, nb, E, block_m, counts, offsets,
+  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scan_kernel, dim3(1), dim3(kChunk), 0, s, bc, nb, E, block_m, counts, offsets,
                      tiles, n_tiles);
   MOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL(align_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
+  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
                      (const int32_t*)bc, perm);
   MOE_CHECK_LAUNCH();
   return MOE_OK;

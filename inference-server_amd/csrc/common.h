@@ -122,8 +122,32 @@ struct WsCarver {
   }
 };
 
+// Kernel slots of the event-timing facility (prof.hip).
+enum {
+  MOE_PROF_ROUTER_GEMM = 0,
+  MOE_PROF_TOPK = 1,
+  MOE_PROF_QUANT_ACT = 2,
+  MOE_PROF_ALIGN = 3,
+  MOE_PROF_GATE_UP = 4,
+  MOE_PROF_QUANT_H = 5,
+  MOE_PROF_DOWN = 6,
+  MOE_PROF_COMBINE = 7,
+  MOE_PROF_SLOTS = 8
+};
+int moe_prof_begin(int slot, hipStream_t s);
+void moe_prof_end(int id, hipStream_t s);
+
+// hipLaunchKernelGGL bracketed by the timing events of `slot` (no-op unless enabled).
+#define MOE_LAUNCH(slot, stream, ...)                  \
+  do {                                                \
+    const int _pid = moe_prof_begin((slot), (stream)); \
+    hipLaunchKernelGGL(__VA_ARGS__);                  \
+    moe_prof_end(_pid, (stream));                     \
+  } while (0)
+
 // Internal launchers shared between translation units.
-int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hipStream_t s);
+int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hipStream_t s,
+                         int slot = MOE_PROF_QUANT_ACT);
 int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
                      int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
                      void* workspace, size_t workspace_bytes, hipStream_t s);

@@ -189,7 +189,8 @@ template <int MODE, int WM, int KS>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   dim3 grid(max_tiles, a.N / (16 * CG));
-  hipLaunchKernelGGL((grouped_gemm_fp8_kernel<MODE, WM, KS>), grid, dim3(256), 0, s, a);
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS>), grid,
+             dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -213,7 +214,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
-  rc = moe_launch_quant_act(h, S, I, hq, sh, s);
+  rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
   if (rc) return rc;
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
   if (block_m == 16)

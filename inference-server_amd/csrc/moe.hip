@@ -113,7 +113,7 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
                                 I, k, w.block_m, s);
   if (rc) return rc;
   const long threads = (long)T * (H / 8);
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+  MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      (const uint16_t*)w.pairs, ids, id_bytes, T, k, H, E, (uint16_t*)out);
   MOE_CHECK_LAUNCH();
   return MOE_OK;

@@ -78,11 +78,11 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const TIn* __restrict
 
 }  // namespace
 
-int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hipStream_t s) {
+int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hipStream_t s, int slot) {
   if (R == 0) return MOE_OK;
   const long n_groups = (long)R * (C / MOE_GROUP);
   const long blocks = (n_groups + 15) / 16;
-  hipLaunchKernelGGL(quant_act_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint16_t*)x,
+  MOE_LAUNCH(slot, s, quant_act_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint16_t*)x,
                      n_groups, C / MOE_GROUP, (uint8_t*)q, scales);
   MOE_CHECK_LAUNCH();
   return MOE_OK;

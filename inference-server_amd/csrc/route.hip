@@ -9,6 +9,7 @@ namespace {
 constexpr int kRouterTileT = 16;    // tokens per MFMA tile
 constexpr int kRouterWaveE = 16;    // experts per wave
 constexpr int kRouterBlockE = 64;   // experts per workgroup (4 waves)
+constexpr int kMaxKSplit = 16;      // router K-split partials summed by the top-k kernel
 
 // partial[z, t, e] = sum over k in chunk z of x[t, k] * w[e, k]   (fp32)
 // grid (ceil(T/16), ceil(E/64), ksplit), block 256.
@@ -77,8 +78,14 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
     lb[c] = 0;
     if (!valid[c]) continue;
     if (part) {
+      // all partial loads issue before the first add: they are independent, and a
+      // load-add chain would pay the cross-XCD load latency ksplit times
+      float pv[kMaxKSplit];
+#pragma unroll
+      for (int z = 0; z < kMaxKSplit; ++z) pv[z] = z < ksplit ? part[((long)z * T + t) * E + e] : 0.f;
       float s = 0.f;
-      for (int z = 0; z < ksplit; ++z) s += part[((long)z * T + t) * E + e];
+#pragma unroll
+      for (int z = 0; z < kMaxKSplit; ++z) s += pv[z];
       lb[c] = f32_to_bf16(s);
       if (logits_out) logits_out[(long)t * E + e] = lb[c];
     } else {
@@ -142,7 +149,8 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
 int route_ksplit(int T, int H, int E) {
   const int tiles = ((T + kRouterTileT - 1) / kRouterTileT) * ((E + kRouterBlockE - 1) / kRouterBlockE);
   int ks = (256 + tiles - 1) / tiles;
-  const int kmax = H / 256 > 0 ? H / 256 : 1;
+  int kmax = H / 256 > 0 ? H / 256 : 1;
+  if (kmax > kMaxKSplit) kmax = kMaxKSplit;
   if (ks > kmax) ks = kmax;
   if (ks < 1) ks = 1;
   return ks;
@@ -176,10 +184,10 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   MOE_RETURN_IF(workspace_bytes < moe_mi355x_route_workspace_bytes(T, H, E) || !workspace, MOE_ERR_WORKSPACE);
   float* part = (float*)workspace;
   dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
-  hipLaunchKernelGGL(router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+  MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
                      (const uint16_t*)w_router, T, H, E, kchunk, part);
   MOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL(topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
+  MOE_LAUNCH(MOE_PROF_TOPK, s, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
                      (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes,
                      (uint16_t*)weights);
   MOE_CHECK_LAUNCH();

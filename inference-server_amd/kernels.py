@@ -24,14 +24,14 @@ def _stream(t: torch.Tensor) -> int:
 def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
-    if t.device.type != "cuda":
-        raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
     if not isinstance(dtypes, (tuple, list)):
         dtypes = (dtypes,)
     if t.dtype not in dtypes:
         raise TypeError(f"{name} must have dtype {' or '.join(map(str, dtypes))}, got {t.dtype}")
     if ndim is not None and t.dim() != ndim:
         raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm GPU device, got {t.device}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 

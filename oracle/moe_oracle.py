@@ -53,10 +53,10 @@ GROUP = 128
 def round_bf16(a) -> np.ndarray:
     """Round float32 values to the nearest bf16 (ties to even), returned as float32."""
     a = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
-    bits = a.view(np.uint32).astype(np.uint64)
-    lsb = (bits >> 16) & 1
-    rounded = ((bits + 0x7FFF + lsb) >> 16) << 16
-    out = rounded.astype(np.uint32).view(np.float32).reshape(a.shape)
+    bits = a.view(np.uint32)
+    # finite inputs cannot overflow 32 bits here; NaNs are restored below
+    rounded = (bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    out = rounded.view(np.float32).reshape(a.shape)
     nan = np.isnan(a)
     if nan.any():
         out = np.where(nan, np.float32(np.nan), out)

@@ -1,0 +1,82 @@
+"""The C-ABI library loads and exports every symbol include/moe_mi355x.h declares (CPU only).
+
+Only host-side paths are called here: queries (sizes, version, error text) and argument
+validation that returns before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "moe_mi355x.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(moe_mi355x_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    from inference_server_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        import __graft_entry__
+
+        __graft_entry__._load_build_module().build()
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for n in ["moe_mi355x_route", "moe_mi355x_topk_softmax", "moe_mi355x_align", "moe_mi355x_quantize_act_fp8",
+              "moe_mi355x_quantize_weight_fp8", "moe_mi355x_experts_fp8", "moe_mi355x_block_fp8"]:
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr)
+
+
+def test_binding_covers_header(pkg):
+    from inference_server_amd import _lib
+
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_host_queries(lib):
+    assert lib.moe_mi355x_version() >= 1
+    assert lib.moe_mi355x_error_string(0) == b"success"
+    assert b"workspace" in lib.moe_mi355x_error_string(-2)
+    assert lib.moe_mi355x_align_max_tiles(8, 128, 16) == 8            # T=1, k=8: one tile per expert
+    assert lib.moe_mi355x_align_max_tiles(32768, 128, 64) == 512 + 128
+    assert lib.moe_mi355x_experts_workspace_bytes(64, 2048, 768, 128, 8) > 64 * 8 * 2048 * 2
+    assert lib.moe_mi355x_experts_workspace_bytes(64, 2000, 768, 128, 8) == 0  # H not a multiple of 128
+    assert lib.moe_mi355x_block_workspace_bytes(64, 2048, 768, 128, 8) > \
+        lib.moe_mi355x_experts_workspace_bytes(64, 2048, 768, 128, 8)
+
+
+def test_argument_validation_before_launch(lib):
+    null = None
+    # unsupported shapes -> MOE_ERR_INVALID_ARG (-1), no device work attempted
+    assert lib.moe_mi355x_experts_fp8(null, null, 4, null, 4, 2000, 768, 128, 8, null, null, null, null, null,
+                                      null, 0, null) == -1
+    assert lib.moe_mi355x_experts_fp8(null, null, 3, null, 4, 2048, 768, 128, 8, null, null, null, null, null,
+                                      null, 0, null) == -1
+    assert lib.moe_mi355x_route(null, null, 4, 2048, 300, 8, 1, null, null, 4, null, null, 0, null) == -1
+    assert lib.moe_mi355x_route(null, null, 4, 2048, 128, 0, 1, null, null, 4, null, null, 0, null) == -1
+    assert lib.moe_mi355x_quantize_act_fp8(null, 4, 100, null, null, null) == -1
+    assert lib.moe_mi355x_quantize_weight_fp8(null, 2, 1, 128, 128, null, null, null) == -1
+    # T == 0 is a successful no-op
+    assert lib.moe_mi355x_experts_fp8(null, null, 4, null, 0, 2048, 768, 128, 8, null, null, null, null, null,
+                                      null, 0, null) == 0
+    # null tensors with T > 0 are rejected
+    assert lib.moe_mi355x_experts_fp8(null, null, 4, null, 1, 2048, 768, 128, 8, null, null, null, null, null,
+                                      null, 0, null) == -1

@@ -1,0 +1,114 @@
+"""The HIP path behind the reference's own call sites (GPU).
+
+* transformers' FP8 experts module dispatching to the ``"mi355x"`` experts implementation
+  (TF/integrations/moe.py:567-570, finegrained_fp8.py:757-768);
+* a tiny Qwen3-MoE causal LM whose sparse blocks were swapped for ``MI355XSparseMoeBlock``,
+  driven the way the reference backend drives it: a prefill forward with a KV cache, then
+  a batched one-token decode step (src/inference_server/backends/torch_backend.py:283-322).
+  Every swapped block's output is checked against the oracle on the block's captured input.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+from tests.helpers import TOL_MAX_ABS, TOL_MEAN_REL, errors, f8_codes, np_f32
+
+pytestmark = pytest.mark.gpu
+
+transformers = pytest.importorskip("transformers")
+
+
+def _tiny_config(**kw):
+    from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
+
+    base = dict(vocab_size=128, hidden_size=256, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+                num_key_value_heads=1, head_dim=128, num_experts=16, num_experts_per_tok=4, moe_intermediate_size=128,
+                norm_topk_prob=True, max_position_embeddings=256)
+    base.update(kw)
+    return Qwen3MoeConfig(**base)
+
+
+def test_fp8_experts_interface_dispatch(pkg, dev):
+    from transformers.integrations.finegrained_fp8 import ALL_FP8_EXPERTS_FUNCTIONS, FP8Experts
+    from transformers.integrations.moe import use_experts_implementation
+
+    assert pkg.register()
+    cfg = _tiny_config()
+    cfg._experts_implementation = pkg.IMPLEMENTATION_KEY
+    cls = use_experts_implementation(experts_class=FP8Experts, experts_interface=ALL_FP8_EXPERTS_FUNCTIONS)
+    mod = cls(cfg, block_size=(128, 128)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    E, I, H = 16, 128, 256
+    w13 = (torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02)
+    w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02)
+    q13, s13 = pkg.quantize_weight_fp8(w13)
+    q2, s2 = pkg.quantize_weight_fp8(w2)
+    with torch.no_grad():
+        mod.gate_up_proj.copy_(q13)
+        mod.gate_up_proj_scale_inv.copy_(s13)
+        mod.down_proj.copy_(q2)
+        mod.down_proj_scale_inv.copy_(s2)
+    T, k = 40, 4
+    x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, device=dev)[:k] for _ in range(T)])  # int64, like torch.topk
+    w = torch.softmax(torch.randn((T, k), generator=g, device=dev), -1).to(torch.bfloat16)
+    out = mod(x, ids, w)
+    assert out.shape == (T, H) and out.dtype == torch.bfloat16
+    ref = orc.experts_fp8(np_f32(x), ids.cpu().numpy(), np_f32(w), f8_codes(q13), s13.cpu().numpy(),
+                          f8_codes(q2), s2.cpu().numpy())
+    max_abs, mean_rel = errors(np_f32(out), ref)
+    assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
+
+
+def test_swapped_model_prefill_and_decode(pkg, dev):
+    from transformers import DynamicCache
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeForCausalLM
+
+    torch.manual_seed(0)
+    cfg = _tiny_config()
+    model = Qwen3MoeForCausalLM(cfg).to(torch.bfloat16).to(dev).eval()
+    with torch.no_grad():
+        for layer in model.model.layers:
+            layer.mlp.gate.weight.normal_(0, 0.02)
+            layer.mlp.experts.gate_up_proj.normal_(0, 0.02)
+            layer.mlp.experts.down_proj.normal_(0, 0.02)
+    assert pkg.swap_moe_blocks(model) == cfg.num_hidden_layers
+    captured = []
+
+    def hook(mod, inp, out):
+        captured.append((mod, inp[0].detach().clone(), out.detach().clone()))
+
+    for layer in model.model.layers:
+        assert isinstance(layer.mlp, pkg.MI355XSparseMoeBlock)
+        layer.mlp.register_forward_hook(hook)
+
+    B, S = 3, 24
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev)
+    cache = DynamicCache()
+    with torch.no_grad():
+        out = model(input_ids=ids, past_key_values=cache, use_cache=True)
+        nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+        out2 = model(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True)
+    assert out.logits.shape == (B, S, cfg.vocab_size)
+    assert out2.logits.shape == (B, 1, cfg.vocab_size)
+    assert torch.isfinite(out2.logits.float()).all()
+    assert len(captured) == 2 * cfg.num_hidden_layers  # prefill + decode per layer
+
+    for mod, x, y in captured:
+        xs = np_f32(x.reshape(-1, cfg.hidden_size))
+        e = mod.experts
+        # feed the GPU's own routing to the oracle experts: bit-exact ids are tested elsewhere
+        _, (glg, gw, gids) = pkg.moe_block_fp8(x, mod.gate.weight, cfg.num_experts_per_tok, e.gate_up_proj,
+                                               e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv,
+                                               return_routing=True)
+        ids_from_gpu_logits, _, _ = orc.topk_from_logits(np_f32(glg), cfg.num_experts_per_tok)
+        np.testing.assert_array_equal(gids.cpu().numpy(), ids_from_gpu_logits)
+        ref = orc.experts_fp8(xs, gids.cpu().numpy(), np_f32(gw), f8_codes(e.gate_up_proj),
+                              e.gate_up_proj_scale_inv.cpu().numpy(), f8_codes(e.down_proj),
+                              e.down_proj_scale_inv.cpu().numpy())
+        max_abs, mean_rel = errors(np_f32(y).reshape(ref.shape), ref)
+        assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
