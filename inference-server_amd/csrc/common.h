@@ -24,15 +24,25 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// Round to nearest even; NaN stays a quiet NaN.
+// Round to nearest even (gfx950 v_cvt_pk_bf16_f32); NaN stays NaN.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
 }
 
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+__device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
+
+// silu(gate) * up on bf16 values, in the reference's rounding order: the grouped GEMM
+// output is bf16, silu(gate) is rounded to bf16, the product is rounded again
+// (TF/integrations/moe.py:509-520).  sigmoid uses v_exp_f32 and v_rcp_f32 (about
+// 1 ulp); the bf16 roundings absorb that except at rare ties.
+__device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
+  const float g = round_bf16(gate_acc);
+  const float u = round_bf16(up_acc);
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  const float sg = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + e));
+  return round_bf16(sg * u);
+}
 
 // ---------------------------------------------------------------------------
 // fp32 -> OCP e4m3fn.  Inputs are clamped to [-448, 448] by the callers, so the
@@ -45,7 +55,7 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
 }
 
 __device__ __forceinline__ float clamp_fp8(float v) {
-  return fminf(fmaxf(v, -MOE_FP8_MAX), MOE_FP8_MAX);
+  return __builtin_amdgcn_fmed3f(v, -MOE_FP8_MAX, MOE_FP8_MAX);
 }
 
 // ---------------------------------------------------------------------------

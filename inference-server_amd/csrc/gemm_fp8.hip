@@ -170,11 +170,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
       if (r >= rows) continue;
       const int srow = row0 + r;
       if constexpr (MODE == MODE_GATE_UP) {
-        // grouped GEMM output is bf16; silu(gate) rounds to bf16; the product rounds again
-        const float g = round_bf16(acc[mi][0][q]);
-        const float u = round_bf16(acc[mi][1][q]);
-        const float sg = round_bf16(g / (1.0f + expf(-g)));
-        p.out[(long)srow * p.N + col] = f32_to_bf16(sg * u);
+        p.out[(long)srow * p.N + col] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
       } else {
         const int pair = p.perm[srow];
         const float z = round_bf16(acc[mi][0][q]);
@@ -197,9 +193,16 @@ int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
 
 }  // namespace
 
-// Tile height (rows per M tile) the grouped GEMMs use for S pairs over E experts.
-int moe_gemm_block_m(int S, int E) {
-  return (S <= 16 * E) ? 16 : 64;
+int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                                     const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
+                                     const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint8_t* hq,
+                                     float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s);
+
+// Tile height (rows per M tile) for S pairs over E experts: 16-row tiles stream weights
+// (decode); 128-row tiles go to the LDS-tiled MFMA kernel (prefill, needs H % 256 == 0).
+int moe_gemm_block_m(int S, int E, int H) {
+  if (S <= 16 * E) return 16;
+  return H % 256 == 0 ? 128 : 64;
 }
 
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
@@ -207,6 +210,9 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
                              const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
                              uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
                              int block_m, hipStream_t s) {
+  if (block_m == 128)
+    return moe_launch_grouped_gemms_prefill(xq, sx, w13, s13, w2, s2, perm, tiles, n_tiles, max_tiles, topk_w, hq,
+                                            sh, pairs, H, I, k, s);
   GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k};
   int rc;
   if (block_m == 16)

@@ -6,7 +6,7 @@
 // and Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
 #include "common.h"
 
-int moe_gemm_block_m(int S, int E);
+int moe_gemm_block_m(int S, int E, int H);
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
                              const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
@@ -73,7 +73,7 @@ struct ExpertsWs {
 ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   ExpertsWs w{};
   const int S = T * k;
-  w.block_m = moe_gemm_block_m(S, E);
+  w.block_m = moe_gemm_block_m(S, E, H);
   w.max_tiles = moe_mi355x_align_max_tiles(S, E, w.block_m);
   WsCarver c(base);
   w.xq = c.take<uint8_t>((size_t)T * H);
@@ -85,7 +85,7 @@ ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   w.n_tiles = c.take<int32_t>(4);
   w.align_ws_bytes = moe_mi355x_align_workspace_bytes(S, E);
   w.align_ws = c.take<char>(w.align_ws_bytes);
-  w.h = c.take<uint16_t>((size_t)S * I);
+  w.h = c.take<uint16_t>(w.block_m == 128 ? 0 : (size_t)S * I);  // the prefill GEMM quantises h in place
   w.hq = c.take<uint8_t>((size_t)S * I);
   w.sh = c.take<float>((size_t)S * (I / MOE_GROUP));
   w.pairs = c.take<uint16_t>((size_t)S * H);

@@ -189,6 +189,26 @@ def test_experts_prefill_skewed_30b(pkg, dev, w30b):
     _check_experts(pkg, dev, x, ids, w, *w30b, idx_subset=sub)
 
 
+@pytest.mark.parametrize("T", [300, 1024])
+def test_experts_prefill_uniform_30b(pkg, dev, w30b, T):
+    """128-row LDS-tiled path (S > 16 E) with ragged last tiles per expert."""
+    rng = np.random.default_rng(20 + T)
+    x = orc.gen_normal_bf16(rng, (T, 2048))
+    ids, w = orc.uniform_routing(rng, T, 128, 8)
+    sub = np.sort(rng.choice(T, min(T, 80), replace=False))
+    _check_experts(pkg, dev, x, ids, w, *w30b, idx_subset=sub)
+
+
+def test_experts_64row_path_odd_hidden(pkg, dev):
+    """H % 256 != 0 takes the 64-row register-tiled path for prefill-sized batches."""
+    E, H, I, k, T = 4, 384, 256, 2, 96
+    q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=5)
+    rng = np.random.default_rng(21)
+    x = orc.gen_normal_bf16(rng, (T, H))
+    ids, w = orc.uniform_routing(rng, T, E, k)
+    _check_experts(pkg, dev, x, ids, w, q13, s13, q2, s2)
+
+
 def test_experts_deterministic(pkg, dev, w30b):
     rng = np.random.default_rng(12)
     T = 300
