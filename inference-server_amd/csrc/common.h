@@ -82,12 +82,78 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// Wave-uniform reductions on the VALU only: DPP row rotations reduce each 16-lane row
+// (every lane ends with its row's result), v_readlane combines the four rows.  No LDS
+// crossbar traffic, unlike ds_bpermute-based shuffles.
+template <int N>
+__device__ __forceinline__ uint32_t row_ror(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+  uint32_t o;
+  o = row_ror<1>(v); v = o > v ? o : v;
+  o = row_ror<2>(v); v = o > v ? o : v;
+  o = row_ror<4>(v); v = o > v ? o : v;
+  o = row_ror<8>(v); v = o > v ? o : v;
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  const uint32_t a = r0 > r1 ? r0 : r1, b = r2 > r3 ? r2 : r3;
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ float wave_max_uniform(float v) {
+  v = fmaxf(v, __uint_as_float(row_ror<1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror<2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror<4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror<8>(__float_as_uint(v))));
+  return fmaxf(fmaxf(__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0)),
+                     __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16))),
+               fmaxf(__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32)),
+                     __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48))));
+}
+
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+  v += __uint_as_float(row_ror<1>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<2>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<4>(__float_as_uint(v)));
+  v += __uint_as_float(row_ror<8>(__float_as_uint(v)));
+  return (__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0)) +
+          __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16))) +
+         (__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32)) +
+          __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48)));
+}
+
 // max over aligned groups of `width` lanes (width a power of two <= 64)
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll
   for (int m = WIDTH / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, MOE_WAVE));
   return v;
+}
+
+// Dynamic e4m3 quantisation of one 128-value group held by 16 adjacent lanes x 8 bf16
+// values (16 bytes at src): s = amax/448 (1 if amax == 0), q = e4m3(clamp(x / s)).
+// Writes 8 codes per lane and, from lane sub == 0, the group scale.
+__device__ __forceinline__ void quant_group16(const uint16_t* src, uint8_t* dst, float* sdst, int sub) {
+  const uint4 raw = *(const uint4*)src;
+  float v[8];
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = group_max<16>(amax);
+  const float s = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
+  uint2 out;  // correctly rounded x / s, as the oracle
+  out.x = pack4_e4m3(clamp_fp8(v[0] / s), clamp_fp8(v[1] / s), clamp_fp8(v[2] / s), clamp_fp8(v[3] / s));
+  out.y = pack4_e4m3(clamp_fp8(v[4] / s), clamp_fp8(v[5] / s), clamp_fp8(v[6] / s), clamp_fp8(v[7] / s));
+  *(uint2*)dst = out;
+  if (sub == 0) *sdst = s;
 }
 
 __device__ __forceinline__ uint64_t lanemask_lt() {

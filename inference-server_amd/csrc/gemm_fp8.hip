@@ -66,6 +66,24 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   __shared__ float s_sa[BM][kMaxKB];         // activation scales of the tile
   __shared__ float s_red[KS > 1 ? (KS - 1) * CG * WM * NOP * 4 * 64 : 1];
 
+  // The weight stream needs only the expert and the column block: its first loads go
+  // out before the activation-row setup (perm -> rows -> scales), whose dependent round
+  // trips then overlap the weight fetch.
+  const uint8_t* bptr[NOP];
+  const float* swp[NOP];
+#pragma unroll
+  for (int o = 0; o < NOP; ++o) {
+    const int wrow = n0 + o * p.N;  // up rows follow the I gate rows
+    bptr[o] = p.w + ((long)e * Nw + wrow + lr) * p.K + lg * 32;
+    swp[o] = p.sw + ((long)e * (Nw / MOE_GROUP) + wrow / MOE_GROUP) * KB;
+  }
+
+  v8i bc[NOP];
+  if (ks < KB) {
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) bc[o] = *(const v8i*)(bptr[o] + ks * MOE_GROUP);
+  }
+
   for (int r = threadIdx.x; r < BM; r += blockDim.x) {
     const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
     s_arow[r] = MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
@@ -80,26 +98,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   const uint8_t* aptr[WM];
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi) aptr[mi] = p.a + (long)s_arow[mi * 16 + lr] * p.K + lg * 32;
-  const uint8_t* bptr[NOP];
-  const float* swp[NOP];
-#pragma unroll
-  for (int o = 0; o < NOP; ++o) {
-    const int wrow = n0 + o * p.N;  // up rows follow the I gate rows
-    bptr[o] = p.w + ((long)e * Nw + wrow + lr) * p.K + lg * 32;
-    swp[o] = p.sw + ((long)e * (Nw / MOE_GROUP) + wrow / MOE_GROUP) * KB;
-  }
-
   v4f acc[WM][NOP];
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi)
 #pragma unroll
     for (int o = 0; o < NOP; ++o) acc[mi][o] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  v8i bc[NOP], ac[WM];
+  v8i ac[WM];
   int kb = ks;
   if (kb < KB) {
-#pragma unroll
-    for (int o = 0; o < NOP; ++o) bc[o] = *(const v8i*)(bptr[o] + kb * MOE_GROUP);
 #pragma unroll
     for (int mi = 0; mi < WM; ++mi) ac[mi] = *(const v8i*)(aptr[mi] + kb * MOE_GROUP);
   }
@@ -185,8 +192,8 @@ template <int MODE, int WM, int KS>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   dim3 grid(max_tiles, a.N / (16 * CG));
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS>), grid,
-             dim3(256), 0, s, a);
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS>),
+             grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -220,6 +227,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
+  // one pass quantises h; quantising it inside the down GEMM instead would repeat the
+  // work in every one of the H/16 column waves that read a row
   rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
   if (rc) return rc;
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};

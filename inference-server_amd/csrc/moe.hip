@@ -14,8 +14,10 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
                              int block_m, hipStream_t s);
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
-                     size_t workspace_bytes, hipStream_t s);
+                     size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
+                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles);
 extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E);
+bool moe_route_can_fuse_align(int T, int E, int k);
 extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m);
 extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E);
 
@@ -31,16 +33,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   if (idx >= (long)T * per_row) return;
   const int t = (int)(idx / per_row), c8 = (int)(idx % per_row);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const int pr = t * k + j;
-    const long id = id_bytes == 8 ? (long)((const int64_t*)ids)[pr] : (long)((const int32_t*)ids)[pr];
-    if (id < 0 || id >= E) continue;
-    const uint4 v = *(const uint4*)(pairs + (long)pr * H + c8 * 8);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  // rows are loaded unconditionally (a sentinel slot's row exists, unwritten) and masked
+  // afterwards, so that the k loads are in flight together rather than one per branch
+  constexpr int kUnroll = 8;
+  for (int j0 = 0; j0 < k; j0 += kUnroll) {
+    uint4 v[kUnroll];
+    bool ok[kUnroll];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] += __uint_as_float(w[i] << 16);
-      acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int pr = t * k + min(j0 + u, k - 1);
+      const long id = id_bytes == 8 ? (long)((const int64_t*)ids)[pr] : (long)((const int32_t*)ids)[pr];
+      ok[u] = j0 + u < k && id >= 0 && id < E;
+      v[u] = *(const uint4*)(pairs + (long)pr * H + c8 * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += ok[u] ? __uint_as_float(w[i] << 16) : 0.f;
+        acc[2 * i + 1] += ok[u] ? __uint_as_float(w[i] & 0xffff0000u) : 0.f;
+      }
     }
   }
   uint4 o;
@@ -99,15 +112,20 @@ bool experts_args_ok(int T, int H, int I, int E, int k, int id_bytes) {
          (long)T * k < (1L << 28);
 }
 
+// Experts after routing.  `prepared` = x already quantised into w.xq/w.sx and the align
+// outputs already written (the block path fuses both into its routing kernels).
 int launch_experts(const void* x, const void* ids, int id_bytes, const void* weights, int T, int H, int I,
                    int E, int k, const void* w13, const float* s13, const void* w2, const float* s2, void* out,
-                   const ExpertsWs& w, hipStream_t s) {
+                   const ExpertsWs& w, hipStream_t s, bool prepared = false) {
   const int S = T * k;
-  int rc = moe_launch_quant_act(x, T, H, w.xq, w.sx, s);
-  if (rc) return rc;
-  rc = moe_launch_align(ids, id_bytes, S, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
-                        w.align_ws, w.align_ws_bytes, s);
-  if (rc) return rc;
+  int rc;
+  if (!prepared) {
+    rc = moe_launch_quant_act(x, T, H, w.xq, w.sx, s);
+    if (rc) return rc;
+    rc = moe_launch_align(ids, id_bytes, S, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
+                          w.align_ws, w.align_ws_bytes, s);
+    if (rc) return rc;
+  }
   rc = moe_launch_grouped_gemms(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2, w.perm, w.tiles,
                                 w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.hq, w.sh, w.pairs, S, H,
                                 I, k, w.block_m, s);
@@ -207,8 +225,17 @@ extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, 
   void* id_out = ids ? ids : (void*)b.ids;
   const int idb = ids ? id_bytes : 4;
   void* wt = weights ? weights : (void*)b.weights;
-  int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s);
-  if (rc) return rc;
   const ExpertsWs w = carve_experts(b.experts_ws, T, H, I, E, k);
-  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s);
+  // decode batches: x quantisation rides in the router GEMM, align in the top-k kernel
+  const bool fused = moe_route_can_fuse_align(T, E, k);
+  int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s,
+                            w.xq, w.sx, w.block_m, fused ? w.perm : nullptr, w.counts, w.offsets, w.tiles,
+                            w.n_tiles);
+  if (rc) return rc;
+  if (!fused) {
+    rc = moe_launch_align(id_out, idb, T * k, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
+                          w.align_ws, w.align_ws_bytes, s);
+    if (rc) return rc;
+  }
+  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s, /*prepared=*/true);
 }

@@ -7,31 +7,12 @@ namespace {
 
 // One 128-column group is handled by 16 lanes x 8 bf16 values.
 __global__ __launch_bounds__(256) void quant_act_kernel(const uint16_t* __restrict__ x, long n_groups,
-                                                        int groups_per_row, uint8_t* __restrict__ q,
-                                                        float* __restrict__ scales) {
+                                                        uint8_t* __restrict__ q, float* __restrict__ scales) {
   const long g = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   if (g >= n_groups) return;  // the 16 lanes of a group leave together
   const long elem = g * MOE_GROUP + sub * 8;  // groups are contiguous: row r, group j -> r*C + j*128
-  const uint4 raw = *(const uint4*)(x + elem);
-  float v[8];
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = __uint_as_float(w[i] << 16);
-    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = group_max<16>(amax);
-  const float s = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
-  uint2 out;
-  out.x = pack4_e4m3(clamp_fp8(v[0] / s), clamp_fp8(v[1] / s), clamp_fp8(v[2] / s), clamp_fp8(v[3] / s));
-  out.y = pack4_e4m3(clamp_fp8(v[4] / s), clamp_fp8(v[5] / s), clamp_fp8(v[6] / s), clamp_fp8(v[7] / s));
-  *(uint2*)(q + elem) = out;
-  if (sub == 0) scales[g] = s;
-  (void)groups_per_row;
+  quant_group16(x + elem, q + elem, scales + g, sub);
 }
 
 // One workgroup per 128x128 tile; thread t owns row t/2, 64 contiguous columns.
@@ -83,7 +64,7 @@ int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hi
   const long n_groups = (long)R * (C / MOE_GROUP);
   const long blocks = (n_groups + 15) / 16;
   MOE_LAUNCH(slot, s, quant_act_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint16_t*)x,
-                     n_groups, C / MOE_GROUP, (uint8_t*)q, scales);
+             n_groups, (uint8_t*)q, scales);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }

@@ -247,6 +247,36 @@ def test_block_matches_oracle(pkg, dev):
     assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
 
 
+@pytest.fixture(scope="module")
+def router30b(dev):
+    g = torch.Generator(device=dev).manual_seed(7)
+    return (torch.randn((128, 2048), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T", [1, 8, 16, 17, 64, 600])
+def test_block_30b_routing_paths(pkg, dev, w30b, router30b, T):
+    """Block forward across the routing variants: top-k + sort fused in one workgroup
+    (T <= 16), separate top-k then single-workgroup sort (T*k <= 4096), and the
+    multi-block sort."""
+    rng = np.random.default_rng(30 + T)
+    x = orc.gen_normal_bf16(rng, (T, 2048))
+    out, (lg, w, ids) = pkg.moe_block_fp8(to_bf16(x, dev), router30b, 8, *w30b, return_routing=True)
+    lg_n = np_f32(lg)
+    lg_ref = orc.router_logits(x, np_f32(router30b))
+    abs_sum = np.abs(x.astype(np.float64)) @ np.abs(np_f32(router30b).astype(np.float64)).T
+    ulp_ref = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(lg_ref), 1e-30))) - 7)
+    assert np.all(np.abs(lg_n - lg_ref) <= ulp_ref + 1e-5 * abs_sum)
+    ids_ref, w_ref, _ = orc.topk_from_logits(lg_n, 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    assert bf16_ulp_diff(np_f32(w), w_ref).max() <= 1
+    sub = np.sort(rng.choice(T, min(T, 48), replace=False))
+    q13, s13, q2, s2 = w30b
+    ref = orc.experts_fp8(x[sub], ids_ref[sub], w_ref[sub], f8_codes(q13), s13.cpu().numpy(), f8_codes(q2),
+                          s2.cpu().numpy(), acc=np.float32)
+    max_abs, mean_rel = errors(np_f32(out)[sub], ref)
+    assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
+
+
 def test_sentinel_pairs_contribute_zero(pkg, dev, w30b):
     rng = np.random.default_rng(15)
     T = 40
