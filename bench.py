@@ -9,7 +9,11 @@ Zipf-skewed prefill chunk (config 3) rides along in ``sweep``.
 Weights are rotated over enough copies that one step's weights never sit in the 256 MB
 last-level cache from an earlier step; inputs rotate too, so routing changes every step.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--no-sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--zipf] [--no-sweep]
+                       [--no-cpu] [--copy-probe]
+  --zipf        apply the calibrated Zipf(s=1.1) router bias to the headline batch (config 3)
+  --copy-probe  first run a plain 256 MiB device copy three times: the reference kernel whose
+                FETCH_SIZE / WRITE_SIZE counters calibrate the traffic measurement
 """
 
 from __future__ import annotations
@@ -208,6 +212,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--zipf", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (expert-parallel sharding "
@@ -222,11 +228,22 @@ def main():
     pkg._lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     layer = Layer(pkg, torch, dev, n_copies=16)
     router = layer.wr
 
     T = args.tokens
-    xs = make_inputs(torch, dev, T, 8)
+    beta = share = None
+    if args.zipf:
+        beta, share = calibrate_zipf(pkg, torch, dev, router, T=T)
+        router = zipf_router(torch, router, beta)
+    xs = make_inputs(torch, dev, T, 8, zipf_beta=beta)
     ms, slots, n_active, n_rot = run_config(pkg, torch, layer, T, args.steps, args.warmup, router, xs)
     line = {
         "metric": METRIC,
@@ -242,9 +259,11 @@ def main():
         "vs_baseline": None,
         "dtype": "fp8_e4m3",
         "data": "synthetic",
-        "config": {"workload": f"qwen3-30b-a3b moe layer, fp8 128x128 block scales, decode batch {T}",
+        "config": {"workload": f"qwen3-30b-a3b moe layer, fp8 128x128 block scales, "
+                               f"{'prefill chunk' if T >= 1024 else 'decode batch'} {T}",
                    "tokens": T, "hidden": H, "experts": E, "top_k": K_TOP, "moe_intermediate": I,
-                   "routing": "router-driven (x~N(0,1), W_r~N(0,0.02): uniform in distribution)",
+                   "routing": (f"zipf s=1.1 router bias, beta={beta:.3f}, top-10 share={share:.3f}" if args.zipf
+                               else "router-driven (x~N(0,1), W_r~N(0,0.02): uniform in distribution)"),
                    "weight_copies_rotated": n_rot, "mean_active_experts": round(n_active, 2)},
         "roofline": roofline_for(T, slots, n_active),
         "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()},
