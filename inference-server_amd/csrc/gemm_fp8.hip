@@ -44,10 +44,12 @@ struct GemmArgs {
 
 constexpr int kMaxKB = 32;  // K <= 4096
 
-template <int MODE, int WM, int KS>
+// DN: 16-column slices per wave in the down GEMM (adjacent), so that a wave streams as
+// many weight bytes per setup as a gate_up wave (which pairs a gate and an up slice).
+template <int MODE, int WM, int KS, int DN = 1>
 __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
-  constexpr int NOP = MODE == MODE_GATE_UP ? 2 : 1;  // B operands per wave (gate, up)
+  constexpr int NOP = MODE == MODE_GATE_UP ? 2 : DN;  // B operands per wave (gate, up | column slices)
   constexpr int BM = 16 * WM;
 
   const int tile = blockIdx.x;
@@ -59,7 +61,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   const int cg = wave % CG, ks = wave / CG;
   const int lr = lane & 15, lg = lane >> 4;
   const int KB = p.K / MOE_GROUP;
-  const int n0 = (blockIdx.y * CG + cg) * 16;
+  constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;  // output columns per wave
+  const int n0 = (blockIdx.y * CG + cg) * WCOLS;
   const int Nw = MODE == MODE_GATE_UP ? 2 * p.N : p.N;
 
   __shared__ int s_arow[BM];                 // activation row of each tile row
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   const float* swp[NOP];
 #pragma unroll
   for (int o = 0; o < NOP; ++o) {
-    const int wrow = n0 + o * p.N;  // up rows follow the I gate rows
+    const int wrow = MODE == MODE_GATE_UP ? n0 + o * p.N : n0 + 16 * o;  // up rows follow the I gate rows
     bptr[o] = p.w + ((long)e * Nw + wrow + lr) * p.K + lg * 32;
     swp[o] = p.sw + ((long)e * (Nw / MOE_GROUP) + wrow / MOE_GROUP) * KB;
   }
@@ -180,19 +183,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
         p.out[(long)srow * p.N + col] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
       } else {
         const int pair = p.perm[srow];
-        const float z = round_bf16(acc[mi][0][q]);
         const float wt = bf16_to_f32(p.topk_w[pair]);
-        p.out[(long)pair * p.N + col] = f32_to_bf16(z * wt);
+#pragma unroll
+        for (int o = 0; o < NOP; ++o)
+          p.out[(long)pair * p.N + col + 16 * o] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
       }
     }
   }
 }
 
-template <int MODE, int WM, int KS>
+template <int MODE, int WM, int KS, int DN = 1>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
-  dim3 grid(max_tiles, a.N / (16 * CG));
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS>),
+  constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;
+  dim3 grid(max_tiles, a.N / (WCOLS * CG));
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN>),
              grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -232,8 +237,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
   if (rc) return rc;
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
-  if (block_m == 16)
-    rc = launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
+    rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
   else
     rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
   return rc;

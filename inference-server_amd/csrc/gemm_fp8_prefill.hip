@@ -58,7 +58,11 @@ struct PrefillArgs {
   int n_nblk;              // column blocks per tile: gate_up I/128, down H/256
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+// LDS rows are 128 bytes = 32 of the 64 four-byte banks, so an MFMA fragment read (16
+// lanes on 16 consecutive rows, one 16-byte chunk each) covers all 64 banks only if the 8
+// even rows and the 8 odd rows each use 8 different chunk positions: chunk c of row r is
+// stored at position c ^ ((r >> 1) & 7).
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
   const uint4 lo = *(const uint4*)(base + swz(row, c0));
@@ -121,10 +125,11 @@ __global__ __launch_bounds__(512, 1) void grouped_gemm_fp8_prefill_kernel(Prefil
   const int my_slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
   const uint32_t lds_stage0 = __builtin_amdgcn_readfirstlane(lds_u32(&s_ab[0][0]));
 
-  // DMA lane assignment: one instruction fills 8 rows x 128 B.  Lane L writes physical
-  // chunk L & 7 of row L >> 3, which holds logical chunk (L & 7) ^ (row & 7).
+  // DMA lane assignment: one instruction fills 8 rows x 128 B (block j = rows 8j..8j+7).
+  // Lane L writes position L & 7 of row 8j + (L >> 3), which holds logical chunk
+  // (L & 7) ^ ((row >> 1) & 7); every block this wave fills has j = wave (mod 2).
   const int dma_r = lane >> 3;
-  const int dma_lc = (lane & 7) ^ dma_r;
+  const int dma_lc = (lane & 7) ^ ((4 * (wave & 1) + (dma_r >> 1)) & 7);
 
   // B row of fragment ni of this wave (within the 256-row B tile)
 #define PF_BROW(ni) \

@@ -55,7 +55,7 @@ int moe_prof_begin(int slot, hipStream_t s) {
 void moe_prof_end(int id, hipStream_t s) {
   if (id < 0) return;
   std::lock_guard<std::mutex> lk(g_mu);
-  if (id < (int)g_recs.size()) hipEventRecord(g_recs[id].b, s);
+  if (id < (int)g_recs.size()) (void)hipEventRecord(g_recs[id].b, s);
 }
 
 extern "C" int moe_mi355x_profile_enable(int on) {
