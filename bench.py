@@ -153,6 +153,39 @@ def run_config(pkg, torch, layer, T, steps, warmup, router, xs, profile_slots=Tr
     return ms, slots, n_active, n_rot
 
 
+def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
+    """Per-step time when every step is a replay of a captured HIP graph (one graph per
+    input / weight-copy pair in the rotation): the launch-bound small batches without
+    the host's per-kernel launch cost."""
+    expected_active = E * (1.0 - (1.0 - K_TOP / E) ** T)
+    n_rot = max(2, min(len(layer.copies), math.ceil(2 * LLC_BYTES / max(1.0, layer_bytes(expected_active, T, H, I, E)))))
+    graphs = []
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for j in range(n_rot):
+            q13, s13, q2, s2 = layer.copies[j]
+            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, q13, s13, q2, s2)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for j in range(n_rot):
+        q13, s13, q2, s2 = layer.copies[j]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, q13, s13, q2, s2)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for i in range(steps):
+        graphs[i % n_rot].replay()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) / steps
+
+
 def roofline_for(T, slots, n_active):
     dom = max(slots, key=slots.get)
     dur_s = slots[dom] * 1e-3
@@ -268,6 +301,7 @@ def main():
         "roofline": roofline_for(T, slots, n_active),
         "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()},
         "layer_hbm_frac": round(layer_bytes(n_active, T, H, I, E) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "us_per_layer_graph": round(graph_step_ms(pkg, torch, layer, T, args.steps, router, xs) * 1e3, 2),
     }
     if not args.no_sweep:
         sweep = []
@@ -279,7 +313,9 @@ def main():
             steps = 20 if Ts < 4096 else 10
             ms_s, slots_s, act_s, _ = run_config(pkg, torch, layer, Ts, steps, 5, r, xs_s)
             rl = roofline_for(Ts, slots_s, act_s)
+            ms_g = graph_step_ms(pkg, torch, layer, Ts, steps, r, xs_s)
             entry = {"tokens": Ts, "us_per_layer": round(ms_s * 1e3, 2), "tokens_per_s": round(Ts / (ms_s * 1e-3), 1),
+                     "us_per_layer_graph": round(ms_g * 1e3, 2),
                      "mean_active_experts": round(act_s, 2), "roofline": rl,
                      "kernels_us": {k: round(v * 1e3, 2) for k, v in slots_s.items()}}
             if skew:
