@@ -1,10 +1,11 @@
 """Benchmark of the MI355X Qwen3-MoE FP8 expert layer (one GPU).
 
-One step = one MoE block forward (router + FP8 experts) of the Qwen3-30B-A3B-shaped layer
-(hidden 2048, 128 experts, top-8, moe_intermediate 768, 128x128 block scales) over one
-batch of synthetic tokens already resident in HBM.  The headline line is the decode batch
-of 64 tokens; a sweep over the other decode batches and the 4096-token
-Zipf-skewed prefill chunk (config 3) rides along in ``sweep``.
+One step = one MoE block forward (router + FP8 experts) over one batch of synthetic
+tokens already resident in HBM.  The headline line is the Qwen3-30B-A3B-shaped layer
+(hidden 2048, 128 experts, top-8, moe_intermediate 768, 128x128 block scales) at a
+decode batch of 64 tokens.  The sweep adds the other decode batches,
+the 4096-token Zipf-skewed prefill chunk (config 3) and the Qwen3-235B-A22B shape
+(hidden 4096, moe_intermediate 1536) at decode 64 and prefill 2048 (config 4).
 
 Weights are rotated over enough copies that one step's weights never sit in the 256 MB
 last-level cache from an earlier step; inputs rotate too, so routing changes every step.
@@ -19,11 +20,13 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--zipf
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
 import sys
 import time
+from dataclasses import dataclass
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
@@ -32,50 +35,77 @@ METRIC = "MoE layer µs + % roofline (HBM GB/s / FP8 MFMA), Qwen3-30B-A3B shape,
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 LLC_BYTES = 256 * 2 ** 20
-
-E, H, I, K_TOP = 128, 2048, 768, 8
-
-
-def expert_bytes(H, I):
-    """Weight + scale bytes of one expert (gate_up and down), 4,719,744 B for the 30B shape."""
-    return 2 * I * H + H * I + 4 * ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128))
+K_TOP = 8
+N_SLOTS = 8  # kernel timing slots of the library (include/moe_mi355x.h)
 
 
-def gate_up_bytes(n_active, T, H, I, k):
-    """Algorithmic HBM bytes of one gate_up launch: active experts' W13 + scales, the fp8
-    activations and their scales read, the bf16 intermediate written."""
-    return (n_active * (2 * I * H + 4 * (2 * I // 128) * (H // 128)) + T * H + 4 * T * (H // 128)
-            + 2 * T * k * I)
+@dataclass(frozen=True)
+class Shape:
+    name: str
+    H: int
+    I: int
+    E: int = 128
+
+    def gate_up_expert_bytes(self):
+        """W13 + its scales of one expert: 3,146,496 B for the 30B shape."""
+        return 2 * self.I * self.H + 4 * (2 * self.I // 128) * (self.H // 128)
+
+    def expert_bytes(self):
+        """W13 + W2 + scales of one expert: 4,719,744 B for the 30B shape."""
+        return self.gate_up_expert_bytes() + self.H * self.I + 4 * (self.H // 128) * (self.I // 128)
+
+    def gate_up_bytes(self, n_active, T):
+        """Algorithmic HBM bytes of one gate_up launch: the active experts' W13 + scales,
+        the fp8 activations and their scales read, the bf16 intermediate written."""
+        return (n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128)
+                + 2 * T * K_TOP * self.I)
+
+    def gate_up_flops(self, T):
+        return 2.0 * T * K_TOP * (2 * self.I) * self.H
+
+    def layer_bytes(self, n_active, T):
+        return n_active * self.expert_bytes() + 2 * self.E * self.H + 4 * T * self.H
+
+    def layer_flops(self, T):
+        return T * K_TOP * (2.0 * self.H * 2 * self.I + 2.0 * self.I * self.H) + 2.0 * T * self.H * self.E
+
+    def expected_active(self, T):
+        return self.E * (1.0 - (1.0 - K_TOP / self.E) ** T)
+
+    def prefill_path(self, T):
+        """True where the library picks the 128-row MFMA-tiled (compute-bound) GEMMs."""
+        return T * K_TOP > 16 * self.E and self.H % 256 == 0
 
 
-def gate_up_flops(T, H, I, k):
-    return 2.0 * T * k * (2 * I) * H
-
-
-def layer_bytes(n_active, T, H, I, E):
-    return n_active * expert_bytes(H, I) + 2 * E * H + 4 * T * H
-
-
-def layer_flops(T, H, I, E, k):
-    return T * k * (2.0 * H * 2 * I + 2.0 * I * H) + 2.0 * T * H * E
+S30B = Shape("qwen3-30b-a3b", 2048, 768)
+S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 
 
 class Layer:
-    def __init__(self, pkg, torch, dev, n_copies):
+    """Router + FP8 experts of one shape, with `n_copies` distinct copies of the experts."""
+
+    def __init__(self, pkg, torch, dev, shape, n_copies):
+        self.shape = shape
+        E, H, I = shape.E, shape.H, shape.I
         g = torch.Generator(device=dev).manual_seed(0)
         self.wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         w13 = (torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-        w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         q13, s13 = pkg.quantize_weight_fp8(w13)
+        del w13
+        w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
         q2, s2 = pkg.quantize_weight_fp8(w2)
-        del w13, w2
+        del w2
         self.copies = [(q13, s13, q2, s2)] + [tuple(t.clone() for t in (q13, s13, q2, s2))
                                              for _ in range(n_copies - 1)]
 
+    def n_rot(self, T):
+        per_step = self.shape.layer_bytes(self.shape.expected_active(T), T)
+        return max(2, min(len(self.copies), math.ceil(2 * LLC_BYTES / max(1.0, per_step))))
 
-def make_inputs(torch, dev, T, n, zipf_beta=None):
+
+def make_inputs(torch, dev, shape, T, n, zipf_beta=None):
     g = torch.Generator(device=dev).manual_seed(1000 + T)
-    xs = [torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    xs = [torch.randn((T, shape.H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
     if zipf_beta is not None:
         for x in xs:  # hidden dim 0 carries a constant 1, router column 0 the Zipf bias
             x[:, 0] = 1.0
@@ -85,6 +115,7 @@ def make_inputs(torch, dev, T, n, zipf_beta=None):
 def zipf_router(torch, wr, beta):
     import numpy as np
 
+    E = wr.shape[0]
     r = np.random.default_rng(0).permutation(E) + 1
     b = torch.tensor(beta * (-1.1 * np.log(r)), dtype=torch.float32, device=wr.device)
     w = wr.clone()
@@ -92,15 +123,15 @@ def zipf_router(torch, wr, beta):
     return w
 
 
-def calibrate_zipf(pkg, torch, dev, wr, T=4096):
+def calibrate_zipf(pkg, torch, dev, layer, T=4096):
     """Bisect beta so that the 10 most loaded experts take 50% of the T*k assignments."""
-    x = make_inputs(torch, dev, T, 1, zipf_beta=0.0)[0]
+    x = make_inputs(torch, dev, layer.shape, T, 1, zipf_beta=0.0)[0]
     lo, hi = 0.0, 8.0
     share = 0.0
     for _ in range(24):
         mid = 0.5 * (lo + hi)
-        _, _, ids = pkg.route(x, zipf_router(torch, wr, mid), K_TOP)
-        cnt = torch.bincount(ids.reshape(-1), minlength=E).sort(descending=True).values
+        _, _, ids = pkg.route(x, zipf_router(torch, layer.wr, mid), K_TOP)
+        cnt = torch.bincount(ids.reshape(-1), minlength=layer.shape.E).sort(descending=True).values
         share = float(cnt[:10].sum()) / (T * K_TOP)
         if share < 0.5:
             lo = mid
@@ -109,12 +140,11 @@ def calibrate_zipf(pkg, torch, dev, wr, T=4096):
     return 0.5 * (lo + hi), share
 
 
-def run_config(pkg, torch, layer, T, steps, warmup, router, xs, profile_slots=True):
-    """Times `steps` block forwards; returns (ms_per_step, per-slot avg ms, mean active experts)."""
+def run_config(pkg, torch, layer, T, steps, warmup, router, xs):
+    """Times `steps` block forwards, then runs them again under the library's per-kernel
+    HIP events.  Returns (ms per step, per-slot average ms, mean active experts, copies)."""
     lib = pkg._lib.load()
-    expected_active = E * (1.0 - (1.0 - K_TOP / E) ** T)
-    per_step = layer_bytes(expected_active, T, H, I, E)
-    n_rot = max(2, min(len(layer.copies), math.ceil(2 * LLC_BYTES / max(1.0, per_step))))
+    n_rot = layer.n_rot(T)
 
     def step(i, routing=False):
         q13, s13, q2, s2 = layer.copies[i % n_rot]
@@ -131,48 +161,39 @@ def run_config(pkg, torch, layer, T, steps, warmup, router, xs, profile_slots=Tr
     torch.cuda.synchronize()
     ms = st.elapsed_time(en) / steps
 
+    lib.moe_mi355x_profile_enable(1)
+    ids_seen = []
+    for i in range(steps):
+        _, (_, _, ids) = step(i, routing=True)
+        ids_seen.append(ids)
+    torch.cuda.synchronize()
     slots = {}
-    active = []
-    if profile_slots:
-        import ctypes
-
-        lib.moe_mi355x_profile_enable(1)
-        ids_seen = []
-        for i in range(steps):
-            _, (_, _, ids) = step(i, routing=True)
-            ids_seen.append(ids)
-        torch.cuda.synchronize()
-        for slot in range(8):
-            n, tot = ctypes.c_int(0), ctypes.c_double(0.0)
-            pkg._lib.check(lib.moe_mi355x_profile_read(slot, ctypes.byref(n), ctypes.byref(tot)), "profile_read")
-            if n.value:
-                slots[lib.moe_mi355x_profile_slot_name(slot).decode()] = tot.value / steps
-        lib.moe_mi355x_profile_enable(0)
-        active = [int(torch.unique(ids).numel()) for ids in ids_seen]
-    n_active = sum(active) / len(active) if active else float("nan")
-    return ms, slots, n_active, n_rot
+    for slot in range(N_SLOTS):
+        n, tot = ctypes.c_int(0), ctypes.c_double(0.0)
+        pkg._lib.check(lib.moe_mi355x_profile_read(slot, ctypes.byref(n), ctypes.byref(tot)), "profile_read")
+        if n.value:
+            slots[lib.moe_mi355x_profile_slot_name(slot).decode()] = tot.value / steps
+    lib.moe_mi355x_profile_enable(0)
+    active = [int(torch.unique(ids).numel()) for ids in ids_seen]
+    return ms, slots, sum(active) / len(active), n_rot
 
 
 def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
-    """Per-step time when every step is a replay of a captured HIP graph (one graph per
-    input / weight-copy pair in the rotation): the launch-bound small batches without
-    the host's per-kernel launch cost."""
-    expected_active = E * (1.0 - (1.0 - K_TOP / E) ** T)
-    n_rot = max(2, min(len(layer.copies), math.ceil(2 * LLC_BYTES / max(1.0, layer_bytes(expected_active, T, H, I, E)))))
-    graphs = []
+    """Per-step time when every step replays a captured HIP graph (one graph per input /
+    weight-copy pair of the rotation): the small batches without host launch cost."""
+    n_rot = layer.n_rot(T)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for j in range(n_rot):
-            q13, s13, q2, s2 = layer.copies[j]
-            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, q13, s13, q2, s2)
+            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, *layer.copies[j])
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
+    graphs = []
     for j in range(n_rot):
-        q13, s13, q2, s2 = layer.copies[j]
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, q13, s13, q2, s2)
+            pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, *layer.copies[j])
         graphs.append(g)
     for g in graphs:
         g.replay()
@@ -186,25 +207,48 @@ def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
     return st.elapsed_time(en) / steps
 
 
-def roofline_for(T, slots, n_active):
-    dom = max(slots, key=slots.get)
-    dur_s = slots[dom] * 1e-3
-    if T >= 1024:  # prefill chunk: the grouped GEMMs are MFMA-bound
-        flops = gate_up_flops(T, H, I, K_TOP)
-        achieved = flops / slots["gemm_gate_up"] / 1e9  # TFLOP/s
+def roofline_for(shape, T, slots, n_active):
+    """Roofline of the dominant kernel, gate_up: HBM-bound on the decode path (bytes of the
+    measured active experts), MFMA-bound on the 128-row prefill path."""
+    dur_ms = slots["gemm_gate_up"]
+    if shape.prefill_path(T):
+        flops = shape.gate_up_flops(T)
+        achieved = flops / dur_ms / 1e9  # TFLOP/s
         return {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
                 "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                "traffic": None, "algorithmic_flop": flops, "avg_us": round(slots["gemm_gate_up"] * 1e3, 2),
-                "dominant": dom}
-    byts = gate_up_bytes(n_active, T, H, I, K_TOP)
-    achieved = byts / (slots["gemm_gate_up"] * 1e-3) / 1e9  # GB/s
+                "traffic": None, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+    byts = shape.gate_up_bytes(n_active, T)
+    achieved = byts / (dur_ms * 1e-3) / 1e9  # GB/s
     return {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "algorithmic_bytes": int(byts), "avg_us": round(slots["gemm_gate_up"] * 1e3, 2), "dominant": dom,
-            "dominant_us": round(dur_s * 1e6, 2)}
+            "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
 
 
-def cpu_baseline(pkg, torch, layer, router, x, budget_s=20.0):
+def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
+    shape = layer.shape
+    beta = share = None
+    router = layer.wr
+    if zipf is not None:
+        beta, share = zipf
+        router = zipf_router(torch, layer.wr, beta)
+    xs = make_inputs(torch, dev, shape, T, 4, zipf_beta=beta)
+    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 5, router, xs)
+    entry = {"shape": shape.name, "tokens": T, "us_per_layer": round(ms * 1e3, 2),
+             "tokens_per_s": round(T / (ms * 1e-3), 1),
+             "us_per_layer_graph": round(graph_step_ms(pkg, torch, layer, T, steps, router, xs) * 1e3, 2),
+             "mean_active_experts": round(act, 2), "roofline": roofline_for(shape, T, slots, act),
+             "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()}}
+    if zipf is not None:
+        entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
+    if shape.prefill_path(T):
+        entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
+    else:
+        entry["layer_hbm_frac"] = round(shape.layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
+    return entry
+
+
+def cpu_baseline(torch, layer, router, x, budget_s=20.0):
     """The CPU oracle (dequantise-then-fp32-matmul restatement of the reference path), timed
     on this host on the headline workload; median over as many steps as fit the budget."""
     import numpy as np
@@ -233,7 +277,7 @@ def cpu_baseline(pkg, torch, layer, router, x, budget_s=20.0):
     med = sorted(times)[len(times) // 2]
     return {"value": round(T / med, 2), "unit": "tokens/s", "us_per_layer": round(med * 1e6, 1),
             "cores": threads, "kind": "port",
-            "sample": f"{len(times)} block forwards of the {T}-token decode batch (numpy oracle: router, "
+            "sample": f"{len(times)} block forwards of the {T}-token batch (numpy oracle: router, "
                       f"per-expert dequantise then fp32 matmul), median"}
 
 
@@ -268,15 +312,16 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    layer = Layer(pkg, torch, dev, n_copies=16)
-    router = layer.wr
+    layer = Layer(pkg, torch, dev, S30B, n_copies=16)
+    shape = layer.shape
 
     T = args.tokens
     beta = share = None
+    router = layer.wr
     if args.zipf:
-        beta, share = calibrate_zipf(pkg, torch, dev, router, T=T)
-        router = zipf_router(torch, router, beta)
-    xs = make_inputs(torch, dev, T, 8, zipf_beta=beta)
+        beta, share = calibrate_zipf(pkg, torch, dev, layer, T=T)
+        router = zipf_router(torch, layer.wr, beta)
+    xs = make_inputs(torch, dev, shape, T, 8, zipf_beta=beta)
     ms, slots, n_active, n_rot = run_config(pkg, torch, layer, T, args.steps, args.warmup, router, xs)
     line = {
         "metric": METRIC,
@@ -292,42 +337,31 @@ def main():
         "vs_baseline": None,
         "dtype": "fp8_e4m3",
         "data": "synthetic",
-        "config": {"workload": f"qwen3-30b-a3b moe layer, fp8 128x128 block scales, "
-                               f"{'prefill chunk' if T >= 1024 else 'decode batch'} {T}",
-                   "tokens": T, "hidden": H, "experts": E, "top_k": K_TOP, "moe_intermediate": I,
+        "config": {"workload": f"{shape.name} moe layer, fp8 128x128 block scales, "
+                               f"{'prefill chunk' if shape.prefill_path(T) else 'decode batch'} {T}",
+                   "tokens": T, "hidden": shape.H, "experts": shape.E, "top_k": K_TOP,
+                   "moe_intermediate": shape.I,
                    "routing": (f"zipf s=1.1 router bias, beta={beta:.3f}, top-10 share={share:.3f}" if args.zipf
                                else "router-driven (x~N(0,1), W_r~N(0,0.02): uniform in distribution)"),
                    "weight_copies_rotated": n_rot, "mean_active_experts": round(n_active, 2)},
-        "roofline": roofline_for(T, slots, n_active),
+        "roofline": roofline_for(shape, T, slots, n_active),
         "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()},
-        "layer_hbm_frac": round(layer_bytes(n_active, T, H, I, E) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_hbm_frac": round(shape.layer_bytes(n_active, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "us_per_layer_graph": round(graph_step_ms(pkg, torch, layer, T, args.steps, router, xs) * 1e3, 2),
     }
     if not args.no_sweep:
         sweep = []
-        beta, share = calibrate_zipf(pkg, torch, dev, router)
+        zipf = calibrate_zipf(pkg, torch, dev, layer)
         for Ts in (1, 8, 32, 64, 128, 256, 4096):
-            skew = Ts == 4096
-            xs_s = make_inputs(torch, dev, Ts, 4, zipf_beta=beta if skew else None)
-            r = zipf_router(torch, router, beta) if skew else router
-            steps = 20 if Ts < 4096 else 10
-            ms_s, slots_s, act_s, _ = run_config(pkg, torch, layer, Ts, steps, 5, r, xs_s)
-            rl = roofline_for(Ts, slots_s, act_s)
-            ms_g = graph_step_ms(pkg, torch, layer, Ts, steps, r, xs_s)
-            entry = {"tokens": Ts, "us_per_layer": round(ms_s * 1e3, 2), "tokens_per_s": round(Ts / (ms_s * 1e-3), 1),
-                     "us_per_layer_graph": round(ms_g * 1e3, 2),
-                     "mean_active_experts": round(act_s, 2), "roofline": rl,
-                     "kernels_us": {k: round(v * 1e3, 2) for k, v in slots_s.items()}}
-            if skew:
-                entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
-                entry["layer_tflops"] = round(layer_flops(Ts, H, I, E, K_TOP) / (ms_s * 1e-3) / 1e12, 1)
-            else:
-                entry["layer_hbm_frac"] = round(layer_bytes(act_s, Ts, H, I, E) / (ms_s * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-            sweep.append(entry)
-            print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
+            sweep.append(sweep_entry(pkg, torch, dev, layer, Ts, 20 if Ts < 4096 else 10,
+                                     zipf=zipf if Ts == 4096 else None))
+        big = Layer(pkg, torch, dev, S235B, n_copies=2)
+        for Ts in (64, 2048):
+            sweep.append(sweep_entry(pkg, torch, dev, big, Ts, 20 if Ts < 2048 else 10))
+        del big
         line["sweep"] = sweep
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(pkg, torch, layer, router, xs[0])
+        line["cpu_baseline"] = cpu_baseline(torch, layer, router, xs[0])
     print(json.dumps(line), flush=True)
 
 
