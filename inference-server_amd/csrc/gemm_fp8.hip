@@ -212,9 +212,11 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
 
 // Tile height (rows per M tile) for S pairs over E experts: 16-row tiles stream weights
 // (decode); 128-row tiles go to the LDS-tiled MFMA kernel (prefill, needs H % 256 == 0).
-int moe_gemm_block_m(int S, int E, int H) {
+int moe_gemm_block_m(int S, int E, int H, int I) {
   if (S <= 16 * E) return 16;
-  return H % 256 == 0 ? 128 : 64;
+  // the 128-row prefill path: 256-column tiles of H, and at least 4 K blocks in each GEMM
+  // for its cross-item DMA pipeline
+  return H % 256 == 0 && H >= 512 && I >= 512 ? 128 : 64;
 }
 
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,

@@ -1,5 +1,5 @@
 // Grouped FP8 GEMMs for prefill chunks (many rows per expert): LDS-tiled, persistent,
-// XCD-aware, MFMA-bound.
+// XCD-aware, software-pipelined, MFMA-bound.
 //
 // Tile: 128 sorted rows of one expert x 256 weight rows x 128-deep K blocks.
 //   gate_up: the 256 weight rows are 128 gate rows [n0, n0+128) and the matching 128 up
@@ -10,17 +10,21 @@
 //   down:    256 output columns; epilogue bf16(z) * routing weight, stored at the pair's
 //            original row t*k+j.
 //
-// Workgroup: 8 waves (2 per SIMD) in a 2x4 grid; a wave owns 64 rows x 64 weight rows
-// = 4 x 4 v_mfma_f32_16x16x128_f8f6f4 tiles per K block, each folded into the fp32
-// accumulator with the (activation row scale x weight tile scale) product.  Two waves
-// per SIMD let one wave's scale FMAs and LDS reads run under the other's MFMAs.
+// Workgroup: 4 waves, one per SIMD, in a 2x2 grid; a wave owns 64 rows x 128 weight rows
+// = 4 x 8 v_mfma_f32_16x16x128_f8f6f4 tiles per K block, each folded into the fp32
+// accumulator with the (activation row scale x weight tile scale) product.  The 64x128
+// wave tile reads 24 KB of LDS per 32 MFMAs (0.75 KB per MFMA).
+//
+// Pipeline, per K block kb: one barrier, after which (1) the DMA of K block kb+3 is issued
+// into the LDS stage kb just vacated, (2) the fragments of K block kb+1 are read from LDS
+// into the second register set, (3) the 32 MFMAs of K block kb run on the first set, with
+// the scale FMAs of each MFMA trailing it.  LDS reads, DMA and MFMA/VALU of one wave thus
+// overlap instead of alternating across barriers.
 //
 // Operands are staged through a ring of three 48.5 KB LDS stages (A 16 KB + B 32 KB +
-// 512 B of activation scales) filled by global->LDS DMA without touching VGPRs: K block
-// kb+2 is in flight while kb is computed, so a load has two compute phases to land; one
-// barrier per K block.  LDS rows are 128 bytes;
-// 16-byte chunk c of row r is stored at chunk c ^ (r & 7), so the 8 lanes that share a
-// LDS cycle in a ds_read_b128 of an MFMA fragment hit 8 different bank groups.
+// 512 B of activation scales) filled by global->LDS DMA without touching VGPRs.  LDS rows
+// are 128 bytes; 16-byte chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), so the
+// lanes that share an LDS cycle in a ds_read_b128 of an MFMA fragment hit distinct banks.
 //
 // Persistent grid: one workgroup per CU (the LDS footprint allows one).  Work items
 // (tile, column block) are handed out so that the workgroups resident on one XCD
@@ -39,6 +43,8 @@ constexpr int P_A = PBM * PBK;       // 16 KB
 constexpr int P_B = PBN * PBK;       // 32 KB
 constexpr int P_STAGE = P_A + P_B;   // 48 KB
 constexpr int kMaxKB = 32;           // K <= 4096
+constexpr int P_WAVES = 8;            // two per SIMD: 2 (rows) x 4 (weight columns)
+constexpr int P_THREADS = 64 * P_WAVES;
 
 struct PrefillArgs {
   const uint8_t* a;        // gate_up: xq [T, K] (token rows); down: hq [S, K] (sorted rows)
@@ -58,11 +64,14 @@ struct PrefillArgs {
   int n_nblk;              // column blocks per tile: gate_up I/128, down H/256
 };
 
-// LDS rows are 128 bytes = 32 of the 64 four-byte banks, so an MFMA fragment read (16
-// lanes on 16 consecutive rows, one 16-byte chunk each) covers all 64 banks only if the 8
-// even rows and the 8 odd rows each use 8 different chunk positions: chunk c of row r is
-// stored at position c ^ ((r >> 1) & 7).
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+// LDS rows are 128 bytes (eight 16-byte chunks).  Chunk c of row r is stored at position
+// c ^ swz_key(r), swz_key(r) = (r ^ ((r >> 3) & 1)) & 7: a ds_read_b128 of an MFMA fragment
+// (16 consecutive rows from a multiple of 16, one chunk column per 16 lanes) then runs
+// without bank conflicts on gfx950 (4 LDS cycles per instruction, measured with
+// SQ_LDS_BANK_CONFLICT; XOR with r & 7 or (r >> 1) & 7 alone costs 8).  The key depends on
+// r & 15 only, so a lane's address within any 16-row group is the same.
+__device__ __forceinline__ int swz_key(int row) { return (row ^ ((row >> 3) & 1)) & 7; }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 128 + ((chunk ^ swz_key(row)) << 4); }
 
 __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
   const uint4 lo = *(const uint4*)(base + swz(row, c0));
@@ -77,238 +86,431 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* base, int row, int c0) {
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) { return (uint32_t)(uintptr_t)((LDS_AS const void*)p); }
 
-// Global -> LDS DMA (gfx950 global_load_lds_dwordx4 / _dword): lane i of the wave writes
-// LDS [m0 + 16 i] (resp. [m0 + 4 i]).  Issued from inline asm so the compiler's
-// wait-count pass does not serialise every LDS read behind it; the kernel waits on
-// vmcnt itself.  M0 is saved and restored around the load.
-__device__ __forceinline__ void dma_b128(const void* g, uint32_t lds) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(g), "s"(lds) : "memory");
+// Global -> LDS DMA (gfx950 global_load_lds_dwordx4 / _dword), address = SGPR base +
+// per-lane 32-bit offset: lane i of the wave writes LDS [m0 + 16 i] (resp. [m0 + 4 i]), with
+// m0 = m0base + OFF.  Issued from inline asm so the compiler does not wait on these loads
+// itself; the kernel waits on vmcnt explicitly.  M0 is declared clobbered.
+template <int OFF>
+__device__ __forceinline__ void dma_b128(uint32_t voff, const void* sbase, uint32_t m0base) {
+  asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(m0base), "n"(OFF) : "memory", "m0");
 }
-__device__ __forceinline__ void dma_b32(const void* g, uint32_t lds) {
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(g), "s"(lds) : "memory");
+template <int OFF>
+__device__ __forceinline__ void dma_b32(uint32_t voff, const void* sbase, uint32_t m0base) {
+  asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(m0base), "n"(OFF) : "memory", "m0");
 }
 
 constexpr int P_SA = PBM * 4;                 // 512 B of activation scales per stage
 constexpr int P_STAGE3 = P_STAGE + P_SA;      // 49664 B
-constexpr int P_DMA_PER_STEP = 7;             // per wave: 2 A + 4 B + 1 scale loads per K block
+constexpr int P_DMA_A = P_A / 1024 / P_WAVES;  // 2 per wave
+constexpr int P_DMA_B = P_B / 1024 / P_WAVES;  // 4 per wave
+constexpr int P_DMA_PER_STEP = P_DMA_A + P_DMA_B + 1;  // + one activation-scale load
 
-// Wait until at most N of this wave's vector loads are outstanding and every LDS access
-// has completed, then barrier.  Loads complete in order, so N = loads issued for the
-// next-but-one K block leaves exactly those in flight.
-template <int N>
-__device__ __forceinline__ void wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+// Wait until at most VM of this wave's vector loads are outstanding (inline asm: the
+// compiler does not track the DMA loads) and every LDS access has completed, then
+// barrier.  The LDS wait is the s_waitcnt builtin (vmcnt 63 = no wait, expcnt 7 = no wait,
+// lgkmcnt 0), issued unconditionally, so the compiler's own wait-count tracking sees that
+// every earlier LDS read is complete on every path.  Loads complete in order.
+constexpr int kWaitLgkm0 = 0xF | (3 << 14) | (7 << 4);
+template <int VM>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(VM) : "memory");
+}
+__device__ __forceinline__ void lds_wait_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Constant-address-space views: uniform loads through them become scalar (SMEM) loads,
+// which are tracked by lgkmcnt and never wait behind the in-flight DMA loads (vmcnt).
+#define CONST_AS __attribute__((address_space(4)))
+__device__ __forceinline__ int const_ld(const int32_t* p, long i) { return ((const CONST_AS int32_t*)p)[i]; }
+__device__ __forceinline__ int4 const_ld4(const int32_t* p, long i) {
+  const CONST_AS int32_t* q = (const CONST_AS int32_t*)p + 4 * i;
+  return make_int4(q[0], q[1], q[2], q[3]);
+}
+
+struct PfItem {
+  int e, row0, rows, nb;
+};
+
+__device__ __forceinline__ PfItem pf_item(const PrefillArgs& p, int item) {
+  const int tile = item / p.n_nblk;
+  const int4 ti = const_ld4(p.tiles, tile);
+  return {ti.x, ti.y, ti.z, item - tile * p.n_nblk};
 }
 
 template <int MODE>
-__global__ __launch_bounds__(512, 1) void grouped_gemm_fp8_prefill_kernel(PrefillArgs p) {
+__global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(PrefillArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_ab[3][P_STAGE3];
-  __shared__ int s_arow[PBM];
-  __shared__ int s_pair[PBM];
-  __shared__ float s_wt[PBM];
+  __shared__ __attribute__((aligned(16))) int s_perm[2][PBM];  // perm rows of the item, by item parity
+  __shared__ __attribute__((aligned(16))) float s_swt[2][2][kMaxKB];  // its weight tile scales, per K block
   __shared__ float s_amax[4][PBM];
-  __shared__ float s_sw[3][kMaxKB];  // weight tile scales of the item: gate / up (or the two down blocks)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keep it in an SGPR
-  const int wm = wave & 1, wn = wave >> 1;  // 2 x 4 waves: rows wm*64, column quarter wn
+  const int wm = wave & 1, wn = wave >> 1;  // 2 x 4 waves: rows wm*64, weight-column quarter wn
   const int lr = lane & 15, lg = lane >> 4;
   const int c0 = 2 * lg;
   const int K = p.K, KB = K / PBK;
   const int Nw = MODE == PF_GATE_UP ? 2 * p.N : p.N;
-  const int n_items = p.n_tiles[0] * p.n_nblk;
+  const int nblk128 = Nw / PBK;
+  const int n_items = const_ld(p.n_tiles, 0) * p.n_nblk;
   const int G = gridDim.x;  // a multiple of 8
   const int my_slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  if (my_slot >= n_items) return;  // workgroup-uniform
+  const int n_my = (n_items - my_slot + G - 1) / G;  // items of this workgroup: my_slot + j G
+  const int S_tot = n_my * KB;                        // K-block steps over all of them
   const uint32_t lds_stage0 = __builtin_amdgcn_readfirstlane(lds_u32(&s_ab[0][0]));
+  const uint32_t lds_perm0 = __builtin_amdgcn_readfirstlane(lds_u32(&s_perm[0][0]));
+  const uint32_t lds_swt0 = __builtin_amdgcn_readfirstlane(lds_u32(&s_swt[0][0][0]));
 
-  // DMA lane assignment: one instruction fills 8 rows x 128 B (block j = rows 8j..8j+7).
-  // Lane L writes position L & 7 of row 8j + (L >> 3), which holds logical chunk
-  // (L & 7) ^ ((row >> 1) & 7); every block this wave fills has j = wave (mod 2).
+  // DMA lane assignment: one instruction fills 8 rows x 128 B (block jb = rows 8jb..8jb+7).
+  // Lane L writes position L & 7 of row 8 jb + (L >> 3), which holds logical chunk
+  // (L & 7) ^ swz_key(row) = (L & 7) ^ ((L >> 3) ^ (jb & 1)).  This wave fills blocks
+  // jb = wave + 8 i, so jb & 1 = wave & 1 for all of them.
   const int dma_r = lane >> 3;
-  const int dma_lc = (lane & 7) ^ ((4 * (wave & 1) + (dma_r >> 1)) & 7);
+  const int dma_lc = (lane & 7) ^ ((dma_r ^ (wave & 1)) & 7);
+  // this lane's byte offset within a 16-row fragment group, for chunk columns c0 and c0 + 1
+  const int frag_off0 = lr * 128 + ((c0 ^ swz_key(lr)) << 4);
+  const int frag_off1 = lr * 128 + (((c0 + 1) ^ swz_key(lr)) << 4);
+  // per-lane B offsets (from the item's weight base) of this wave's blocks wave + 8 i:
+  // gate_up tile rows 128.. are the up rows, I - 128 rows further on
+  uint32_t b_voff[P_DMA_B];
+#pragma unroll
+  for (int i = 0; i < P_DMA_B; ++i) {
+    const int br = 8 * (wave + 8 * i);
+    const int wrow = MODE == PF_GATE_UP && br >= 128 ? p.N - 128 + br : br;
+    b_voff[i] = (uint32_t)((wrow + dma_r) * K + dma_lc * 16);
+  }
 
-  // B row of fragment ni of this wave (within the 256-row B tile)
+  // MFMA operand order: the weight fragment is the MFMA's A operand and the activation
+  // fragment its B operand, so the 16x16 result tile is (weight column n, token row m) and
+  // lane l holds columns n = 4 (l >> 4) + q, q = 0..3, of token row m = l & 15: four
+  // consecutive output columns of one row per lane.
+  // Weight row (within the 256-row tile) of fragment ni of this wave: gate_up gate rows
+  // wn*32 + 16 ni (ni < 2) and the matching up rows 128 + wn*32 + 16 (ni - 2); down wn*64 + 16 ni.
 #define PF_BROW(ni) \
   ((MODE == PF_GATE_UP ? ((ni) < 2 ? wn * 32 + (ni) * 16 : 128 + wn * 32 + ((ni) - 2) * 16) : wn * 64 + (ni) * 16) + lr)
 
-  for (int base = 0;; base += G) {
-    const int item = base + my_slot;
-    if (item >= n_items) break;  // workgroup-uniform
-    const int tile = item / p.n_nblk, nb = item - tile * p.n_nblk;
-    const int4 ti = *(const int4*)(p.tiles + 4 * tile);
-    const int e = ti.x, row0 = ti.y, rows = ti.z;
+  // ---- issue side: the item whose K blocks are being loaded ----
+  uint32_t a_voff[P_DMA_A];  // per-lane A byte offsets of this wave's DMA blocks (wave + 8 i)
+  uint32_t sa_voff;          // per-lane activation-scale byte offset (lanes < 16)
+  const uint8_t* wbase;      // uniform: weight row of tile row 0 (gate_up: the gate half)
 
-    __syncthreads();  // the previous item's epilogue is done with the row tables
-    if (tid < PBM) {
-      const int rr = row0 + min(tid, rows - 1);  // rows past the tile end repeat the last row
-      if constexpr (MODE == PF_GATE_UP) {
-        s_arow[tid] = p.perm[rr] / p.topk;
-      } else {
-        s_arow[tid] = rr;
-        const int pr = p.perm[rr];
-        s_pair[tid] = pr;
-        s_wt[tid] = bf16_to_f32(p.topk_w[pr]);
-      }
-    } else if (tid < PBM + 2 * kMaxKB) {
-      // weight tile scales for every K block: gate_up -> gate block nb and up block I/128 + nb;
-      // down -> blocks 2 nb and 2 nb + 1 (the two 128-row halves of the 256 columns)
-      const int j = tid - PBM, which = j / kMaxKB, kb = j % kMaxKB;
-      const int nblk128 = Nw / PBK;
-      const int blk = MODE == PF_GATE_UP ? (which == 0 ? nb : p.N / PBK + nb) : 2 * nb + which;
-      if (kb < KB) s_sw[which][kb] = p.sw[((long)e * nblk128 + blk) * KB + kb];
-    }
-    __syncthreads();
-
-    // per-lane source rows of this wave's DMA instructions (A: blocks wave, wave+8;
-    // B: blocks wave + 8 i; scales: rows 16 wave + lane for lane < 16)
-    const uint8_t* a_src0 = p.a + (long)s_arow[8 * wave + dma_r] * K + dma_lc * 16;
-    const uint8_t* a_src1 = p.a + (long)s_arow[8 * (wave + 8) + dma_r] * K + dma_lc * 16;
-    const uint8_t* b_src[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int br = 8 * (wave + 8 * i) + dma_r;
-      long wrow;
-      if constexpr (MODE == PF_GATE_UP)
-        wrow = br < 128 ? nb * 128 + br : p.N + nb * 128 + (br - 128);
-      else
-        wrow = (long)nb * 256 + br;
-      b_src[i] = p.w + ((long)e * Nw + wrow) * K + dma_lc * 16;
-    }
-    const float* sa_src = p.sa + (long)s_arow[16 * wave + (lane & 15)] * KB;
-
-    // this wave's weight scale rows in s_sw: gate_up (gate, up); down (its 128-column half)
-    const float* sw0 = MODE == PF_GATE_UP ? s_sw[0] : s_sw[wn >> 1];
-    const float* sw1 = MODE == PF_GATE_UP ? s_sw[1] : s_sw[wn >> 1];
-
-#define PF_ISSUE(kb_)                                                                          \
-  do {                                                                                         \
-    const int st_ = (kb_) % 3;                                                                 \
-    const uint32_t sb = lds_stage0 + st_ * P_STAGE3;                                           \
-    const long ko = (long)(kb_) * PBK;                                                         \
-    dma_b128(a_src0 + ko, sb + 1024 * wave);                                                   \
-    dma_b128(a_src1 + ko, sb + 1024 * (wave + 8));                                             \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) dma_b128(b_src[i] + ko, sb + P_A + 1024 * (wave + 8 * i)); \
-    if (lane < 16) dma_b32(sa_src + (kb_), sb + P_STAGE + 64 * wave);                          \
+  // tables of item j -> slot j & 1: its perm rows (rows past the tile end repeat the last
+  // row) and the weight tile scales of all its K blocks (waves 0 and 1: gate_up gate block nb
+  // and up block I/128 + nb; down blocks 2 nb and 2 nb + 1, the two 128-row halves)
+#define PF_TABLE(it_, j_)                                                                         \
+  do {                                                                                            \
+    const int r_ = 16 * wave + lr;                                                                \
+    if (lane < 16)                                                                                \
+      dma_b32<0>((uint32_t)((it_).row0 + min(r_, (it_).rows - 1)) * 4u, p.perm,                  \
+                 lds_perm0 + ((j_) & 1) * (PBM * 4) + 64 * wave);                                 \
+    if (wave < 2 && lane < KB) {                                                                  \
+      const int blk_ = MODE == PF_GATE_UP ? (wave == 0 ? (it_).nb : p.N / PBK + (it_).nb) : 2 * (it_).nb + wave; \
+      dma_b32<0>((uint32_t)(((it_).e * nblk128 + blk_) * KB + lane) * 4u, p.sw,                  \
+                 lds_swt0 + (((j_) & 1) * 2 + wave) * (kMaxKB * 4));                              \
+    }                                                                                             \
   } while (0)
 
-    v4f acc[4][4];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (v4f){0.f, 0.f, 0.f, 0.f};
+  // per-lane DMA offsets of item it_ (its table is in s_perm[j_ & 1] and visible)
+#define PF_DESC(it_, j_)                                                                          \
+  do {                                                                                            \
+    _Pragma("unroll") for (int i = 0; i < P_DMA_A; ++i) {                                         \
+      const int r_ = 8 * (wave + 8 * i) + dma_r;                                                  \
+      const int arow_ = MODE == PF_GATE_UP ? s_perm[(j_) & 1][r_] / p.topk                        \
+                                           : (it_).row0 + min(r_, (it_).rows - 1);                \
+      a_voff[i] = (uint32_t)(arow_ * K + dma_lc * 16);                                            \
+    }                                                                                             \
+    const int rs_ = 16 * wave + lr;                                                               \
+    const int srow_ = MODE == PF_GATE_UP ? s_perm[(j_) & 1][rs_] / p.topk                         \
+                                         : (it_).row0 + min(rs_, (it_).rows - 1);                 \
+    sa_voff = (uint32_t)(srow_ * KB) * 4u;                                                        \
+    wbase = p.w + ((long)(it_).e * Nw + (long)(it_).nb * (MODE == PF_GATE_UP ? 128 : 256)) * K;   \
+  } while (0)
 
-    PF_ISSUE(0);
-    if (KB > 1) {
-      PF_ISSUE(1);
-      wait_barrier<P_DMA_PER_STEP>();
-    } else {
-      wait_barrier<0>();
-    }
-    for (int kb = 0; kb < KB; ++kb) {
-      const bool issue = kb + 2 < KB;
-      if (issue) PF_ISSUE(kb + 2);
-      const uint8_t* sA = s_ab[kb % 3];
-      const uint8_t* sB = sA + P_A;
-      const float* sSa = (const float*)(sA + P_STAGE);
-      v8i a[4], b[4];
+  // one of the 7 DMA instructions of a K block, by index d_ (0..1 A, 2..5 B, 6 scales), with
+  // the bases of the K block computed (sbw_: this wave's first block in the stage)
+#define PF_DMA_ONE(d_, ab_, bb_, sab_, sbw_)                                                      \
+  do {                                                                                            \
+    if constexpr ((d_) < P_DMA_A) dma_b128<(d_) * 8192>(a_voff[d_], ab_, sbw_);                   \
+    else if constexpr ((d_) < P_DMA_A + P_DMA_B)                                                  \
+      dma_b128<P_A + ((d_) - P_DMA_A) * 8192>(b_voff[(d_) - P_DMA_A], bb_, sbw_);                 \
+    else if (lane < 16) dma_b32<0>(sa_voff, sab_, (sbw_) - 1024 * wave + P_STAGE + 64 * wave);    \
+  } while (0)
+
+  // weight tile scales of K block kb_ of item j_ for this wave: gate_up (gate, up); down the
+  // 128-row half of the wave's columns
+#define PF_SW(SW_, j_, kb_)                                                                       \
+  do {                                                                                            \
+    if constexpr (MODE == PF_GATE_UP) {                                                           \
+      SW_[0] = s_swt[(j_) & 1][0][kb_];                                                           \
+      SW_[1] = s_swt[(j_) & 1][1][kb_];                                                           \
+    } else {                                                                                      \
+      SW_[0] = SW_[1] = s_swt[(j_) & 1][wn >> 1][kb_];                                            \
+    }                                                                                             \
+  } while (0)
+
+  // fragments and activation scales of the K block in stage st_ (the four token rows
+  // wm*64 + mi*16 + lr of this lane)
+#define PF_READ(A_, B_, SV_, st_)                                                                 \
+  do {                                                                                            \
+    const uint8_t* sA_ = s_ab[st_];                                                               \
+    const uint8_t* sB_ = sA_ + P_A;                                                               \
+    const float* sS_ = (const float*)(sA_ + P_STAGE);                                             \
+    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) A_[mi] = lds_frag(sA_, wm * 64 + mi * 16 + lr, c0); \
+    _Pragma("unroll") for (int ni = 0; ni < 4; ++ni) B_[ni] = lds_frag(sB_, PF_BROW(ni), c0);     \
+    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) SV_[mi] = sS_[wm * 64 + mi * 16 + lr];       \
+  } while (0)
+
+  // One step's 16 MFMAs (A fragments AC, B fragments B, scales SC/WC; MFMA order ni-major)
+  // with the LDS reads of the next step's fragments (A into AN; each B fragment in place
+  // two slots after its last MFMA of this step), the DMA of K block s+3 and the scale FMAs
+  // interleaved in a fixed order: per slot an MFMA, one LDS read, every other slot a DMA,
+  // then the FMAs of the MFMA three slots back (its result is ready by then).
+  // sched_barrier pins the order.
+#define PF_RD_A(AN_, mi_, h_)                                                                     \
+  do {                                                                                            \
+    const uint4 v_ = *(const uint4*)(sA_ + (wm * 64 + (mi_) * 16) * 128 + ((h_) ? frag_off1 : frag_off0)); \
+    AN_[mi_][4 * (h_)] = v_.x; AN_[mi_][4 * (h_) + 1] = v_.y; AN_[mi_][4 * (h_) + 2] = v_.z; AN_[mi_][4 * (h_) + 3] = v_.w; \
+  } while (0)
+#define PF_RD_B(B_, ni_, h_)                                                                      \
+  do {                                                                                            \
+    const uint4 v_ = *(const uint4*)(sB_ + (PF_BROW(ni_) - lr) * 128 + ((h_) ? frag_off1 : frag_off0)); \
+    B_[ni_][4 * (h_)] = v_.x; B_[ni_][4 * (h_) + 1] = v_.y; B_[ni_][4 * (h_) + 2] = v_.z; B_[ni_][4 * (h_) + 3] = v_.w; \
+  } while (0)
+#define PF_STEP_BODY(AC, AN, B, SC, SN, WC, WN, st_, j1_, kb1_, ab_, bb_, sab_, sbw_)             \
+  do {                                                                                            \
+    const uint8_t* sA_ = s_ab[st_];                                                               \
+    const uint8_t* sB_ = sA_ + P_A;                                                               \
+    const float* sS_ = (const float*)(sA_ + P_STAGE);                                             \
+    float sca_[4], scb_[4];                                                                       \
+    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                            \
+      sca_[mi] = SC[mi] * WC[0];                                                                  \
+      scb_[mi] = MODE == PF_GATE_UP ? SC[mi] * WC[1] : sca_[mi];                                  \
+    }                                                                                             \
+    v4f t_[4];                                                                                    \
+    _Pragma("unroll") for (int it = 0; it < 21; ++it) {                                           \
+      if (it < 16) {                                                                              \
+        const int ni = it >> 2, mi = it & 3;                                                      \
+        t_[it & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(B[ni], AC[mi], zero4, 0, 0, 0, 0, 0, 0); \
+      }                                                                                           \
+      switch (it) {                                                                               \
+        case 0: PF_RD_A(AN, 0, 0); break;                                                         \
+        case 1: PF_RD_A(AN, 0, 1); break;                                                         \
+        case 2: PF_RD_A(AN, 1, 0); break;                                                         \
+        case 3: PF_RD_A(AN, 1, 1); break;                                                         \
+        case 4: PF_RD_A(AN, 2, 0); break;                                                         \
+        case 5: PF_RD_B(B, 0, 0); break;                                                          \
+        case 6: PF_RD_B(B, 0, 1); break;                                                          \
+        case 7: PF_RD_A(AN, 2, 1); break;                                                         \
+        case 8: PF_RD_A(AN, 3, 0); break;                                                         \
+        case 9: PF_RD_B(B, 1, 0); break;                                                          \
+        case 10: PF_RD_B(B, 1, 1); break;                                                         \
+        case 11: PF_RD_A(AN, 3, 1); break;                                                        \
+        case 12: SN[0] = sS_[wm * 64 + lr]; break;                                                \
+        case 13: PF_RD_B(B, 2, 0); break;                                                         \
+        case 14: PF_RD_B(B, 2, 1); break;                                                         \
+        case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                           \
+        case 16: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                           \
+        case 17: PF_RD_B(B, 3, 0); break;                                                         \
+        case 18: PF_RD_B(B, 3, 1); break;                                                         \
+        case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                           \
+        default: PF_SW(WN, j1_, kb1_); break;                                                     \
+      }                                                                                           \
+      if (it == 1) PF_DMA_ONE(0, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 3) PF_DMA_ONE(1, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 5) PF_DMA_ONE(2, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 7) PF_DMA_ONE(3, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 9) PF_DMA_ONE(4, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 11) PF_DMA_ONE(5, ab_, bb_, sab_, sbw_);                                          \
+      if (it == 13) PF_DMA_ONE(6, ab_, bb_, sab_, sbw_);                                          \
+      if (it >= 3 && it < 19) {                                                                   \
+        const int j = it - 3, ni = j >> 2, mi = j & 3;                                            \
+        const float sc_ = (MODE == PF_GATE_UP && ni >= 2) ? scb_[mi] : sca_[mi];                  \
+        _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[mi][ni][q] = fmaf(t_[j & 3][q], sc_, acc[mi][ni][q]); \
+      }                                                                                           \
+      __builtin_amdgcn_sched_barrier(0);                                                          \
+    }                                                                                             \
+  } while (0)
+
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[4][4];
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) a[mi] = lds_frag(sA, wm * 64 + mi * 16 + lr, c0);
+  for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) b[ni] = lds_frag(sB, PF_BROW(ni), c0);
-      float4 sv[4];
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero4;
+  v8i a0[4], a1[4], bf[4];
+  float sv0[4], sv1[4];
+  float sw_0[2], sw_1[2];
+
+  // ---- prologue: item 0's table, its descriptors, K blocks 0..2 in flight ----
+  PfItem it_c = pf_item(p, my_slot);  // the item being computed
+  PfItem it_i = it_c;                 // the item being issued
+  PF_TABLE(it_c, 0);
+  wait_vm<0>();
+  lds_wait_barrier();
+  PF_DESC(it_i, 0);
+  // K blocks 0..2 of item 0 (the pipelined path needs KB >= 4, checked by the launcher)
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) sv[mi] = *(const float4*)&sSa[wm * 64 + mi * 16 + 4 * lg];
-      const float sw_a = sw0[kb], sw_b = sw1[kb];
-      // combined (activation row x weight tile) scale of every accumulator row, per B half
-      float sca[4][4], scb[4][4];
+  for (int k0 = 0; k0 < 3; ++k0) {
+    const uint8_t* ab_ = p.a + (long)k0 * PBK;
+    const uint8_t* bb_ = wbase + (long)k0 * PBK;
+    const float* sab_ = p.sa + k0;
+    const uint32_t sbw_ = lds_stage0 + k0 * P_STAGE3 + 1024 * wave;
+    PF_DMA_ONE(0, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(1, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(2, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(3, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(4, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(5, ab_, bb_, sab_, sbw_);
+    PF_DMA_ONE(6, ab_, bb_, sab_, sbw_);
+  }
+  wait_vm<2 * P_DMA_PER_STEP>();
+  lds_wait_barrier();
+  PF_READ(a0, bf, sv0, 0);
+  PF_SW(sw_0, 0, 0);
+
+  // step counters (uniform): compute step s = K block kb of item j in stage st; issue
+  // target s+3 = K block kb3 of item j3, also into stage st
+  int s = 0, j = 0, kb = 0, st = 0, j3 = 0, kb3 = 3;
+
+  // Step s: wait until K block s+1 has landed (s+2 may stay in flight) and this wave's
+  // fragment reads of s are done; at kb = 0 start the table DMA of item j+1; refill stage
+  // st with K block s+3 (switching the issue side to item j+1 at its first K block) and
+  // read the fragments of s+1 while computing s; at kb = KB-1 run item j's epilogue.
+  // Loads complete in order, so the wait counts are exact.
+#define PF_STEP(AC, AN, SC, SN, WC, WN)                                                           \
+  do {                                                                                            \
+    if (s + 2 < S_tot)                                                                            \
+      wait_vm<P_DMA_PER_STEP>();                                                                  \
+    else                                                                                          \
+      wait_vm<0>();                                                                               \
+    lds_wait_barrier();                                                                           \
+    if (kb == 0 && j + 1 < n_my) {                                                                \
+      const PfItem nx_ = pf_item(p, my_slot + (j + 1) * G);                                       \
+      PF_TABLE(nx_, j + 1);                                                                       \
+    }                                                                                             \
+    /* DMA target: K block s+3; past the last step the stage just freed is refilled with */      \
+    /* a valid block again (no branch in the step body), waited for by the tail's vmcnt(0) */     \
+    const int live_ = s + 3 < S_tot;                                                              \
+    if (live_ && kb3 == 0) {                                                                      \
+      it_i = pf_item(p, my_slot + j3 * G);                                                        \
+      PF_DESC(it_i, j3);                                                                          \
+    }                                                                                             \
+    const int kbi_ = live_ ? kb3 : KB - 1;                                                        \
+    const uint8_t* ab_ = p.a + (long)kbi_ * PBK;                                                  \
+    const uint8_t* bb_ = wbase + (long)kbi_ * PBK;                                                \
+    const float* sab_ = p.sa + kbi_;                                                              \
+    const uint32_t sbw_ = lds_stage0 + st * P_STAGE3 + 1024 * wave;                               \
+    if (live_ && ++kb3 == KB) {                                                                   \
+      kb3 = 0;                                                                                    \
+      ++j3;                                                                                       \
+    }                                                                                             \
+    const int last_ = kb == KB - 1;                                                               \
+    const int st1_ = st == 2 ? 0 : st + 1;                                                        \
+    /* fragments of step s+1 (past the last step: a harmless read of a stale stage) */           \
+    PF_STEP_BODY(AC, AN, bf, SC, SN, WC, WN, st1_, j + last_, last_ ? 0 : kb + 1, ab_, bb_, sab_, sbw_); \
+    if (last_) {                                                                                  \
+      pf_epilogue(j);                                                                             \
+      _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                            \
+        _Pragma("unroll") for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = zero4;                     \
+      ++j;                                                                                        \
+      kb = 0;                                                                                     \
+      if (j < n_my) it_c = pf_item(p, my_slot + j * G);                                           \
+    } else {                                                                                      \
+      ++kb;                                                                                       \
+    }                                                                                             \
+    st = st1_;                                                                                    \
+    ++s;                                                                                          \
+  } while (0)
+
+  // epilogue of item j (it_c), straight from the accumulators: lane holds, for token rows
+  // r = wm*64 + mi*16 + lr, the columns 16 ni + 4 lg + q of this wave's weight rows
+  auto pf_epilogue = [&](int jj) __attribute__((always_inline)) {
+    const int row0 = it_c.row0, rows = it_c.rows, nb = it_c.nb;
+    if constexpr (MODE == PF_GATE_UP) {
+      // h = bf16(bf16(silu(bf16 g)) * bf16 u): gate frags 0, 1 pair with up frags 2, 3, so
+      // this wave holds h columns wn*32 + 16 ni + 4 lg + q
+      float rmax[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
-        const float s4[4] = {sv[mi].x, sv[mi].y, sv[mi].z, sv[mi].w};
+        float m = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          sca[mi][q] = s4[q] * sw_a;
-          scb[mi][q] = MODE == PF_GATE_UP ? s4[q] * sw_b : sca[mi][q];
-        }
-      }
+        for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) {
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi) {
-          const v4f zero = {0.f, 0.f, 0.f, 0.f};
-          const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], b[ni], zero, 0, 0, 0, 0, 0, 0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            acc[mi][ni][q] = fmaf(t[q], (MODE == PF_GATE_UP && ni >= 2) ? scb[mi][q] : sca[mi][q], acc[mi][ni][q]);
-        }
-      }
-      if (issue)
-        wait_barrier<P_DMA_PER_STEP>();
-      else
-        wait_barrier<0>();
-    }
-#undef PF_ISSUE
-
-    if constexpr (MODE == PF_GATE_UP) {
-      // h = bf16(bf16(silu(bf16 g)) * bf16 u) in acc[..][0..1]; gate frags 0,1 pair with up frags 2,3
-      float rmax[4][4];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float m = 0.f;
-#pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
+          for (int q = 0; q < 4; ++q) {
             const float h = silu_mul_bf16(acc[mi][ni][q], acc[mi][ni + 2][q]);
             acc[mi][ni][q] = h;
             m = fmaxf(m, fabsf(h));
           }
-          rmax[mi][q] = group_max<16>(m);  // the 16 lanes sharing these rows
-        }
-      if (lr == 0) {
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) s_amax[wn][wm * 64 + mi * 16 + 4 * lg + q] = rmax[mi][q];
+        // the four lanes lr, lr+16, lr+32, lr+48 share the row
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        rmax[mi] = m;
       }
-      __syncthreads();
+      if (lg == 0) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+        for (int mi = 0; mi < 4; ++mi) s_amax[wn][wm * 64 + mi * 16 + lr] = rmax[mi];
+      }
+      lds_wait_barrier();
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = wm * 64 + mi * 16 + 4 * lg + q;
-          const float amax = fmaxf(fmaxf(s_amax[0][r], s_amax[1][r]), fmaxf(s_amax[2][r], s_amax[3][r]));
-          const float s = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
-          if (r < rows) {
-            const long srow = row0 + r;
-            uint8_t* dst = p.hq + srow * p.N + nb * 128 + wn * 32 + lr;
-            // h * (1/s) with a correctly rounded 1/s: within one fp32 ulp of h / s
-            const float inv_s = 1.0f / s;
-            const int code = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(acc[mi][0][q] * inv_s),
-                                                             clamp_fp8(acc[mi][1][q] * inv_s), 0, false);
-            dst[0] = (uint8_t)(code & 0xff);
-            dst[16] = (uint8_t)((code >> 8) & 0xff);
-            if (wn == 0 && lr == 0) p.sh[srow * (p.N / PBK) + nb] = s;
+      for (int mi = 0; mi < 4; ++mi) {
+        const int r = wm * 64 + mi * 16 + lr;
+        const float amax = fmaxf(fmaxf(s_amax[0][r], s_amax[1][r]), fmaxf(s_amax[2][r], s_amax[3][r]));
+        const float sc = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
+        if (r < rows) {
+          const long srow = row0 + r;
+          // h * (1/s) with a correctly rounded 1/s: within one fp32 ulp of h / s
+          const float inv_s = 1.0f / sc;
+          uint8_t* dst = p.hq + srow * p.N + nb * 128 + wn * 32 + 4 * lg;
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni) {
+            int code = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(acc[mi][ni][0] * inv_s),
+                                                       clamp_fp8(acc[mi][ni][1] * inv_s), 0, false);
+            code = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(acc[mi][ni][2] * inv_s),
+                                                   clamp_fp8(acc[mi][ni][3] * inv_s), code, true);
+            *(int*)(dst + ni * 16) = code;
+          }
+          if (wn == 0 && lg == 0) p.sh[srow * (p.N / PBK) + nb] = sc;
+        }
+      }
+    } else {
+      // bf16(z) at the pair's row; the combine applies the routing weight
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int r = wm * 64 + mi * 16 + lr;
+        if (r < rows) {
+          const long pr = s_perm[jj & 1][r];
+          uint16_t* dst = p.pairs + pr * p.N + nb * 256 + wn * 64 + 4 * lg;
+#pragma unroll
+          for (int ni = 0; ni < 4; ++ni) {
+            uint2 v;
+            v.x = (uint32_t)f32_to_bf16(acc[mi][ni][0]) | ((uint32_t)f32_to_bf16(acc[mi][ni][1]) << 16);
+            v.y = (uint32_t)f32_to_bf16(acc[mi][ni][2]) | ((uint32_t)f32_to_bf16(acc[mi][ni][3]) << 16);
+            *(uint2*)(dst + ni * 16) = v;
           }
         }
-    } else {
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int r = wm * 64 + mi * 16 + 4 * lg + q;
-          if (r >= rows) continue;
-          const long pr = s_pair[r];
-          const float wt = s_wt[r];
-          uint16_t* dst = p.pairs + pr * p.N + nb * 256 + wn * 64 + lr;
-#pragma unroll
-          for (int ni = 0; ni < 4; ++ni) dst[ni * 16] = f32_to_bf16(round_bf16(acc[mi][ni][q]) * wt);
-        }
+      }
     }
+  };
+
+  while (s < S_tot) {
+    PF_STEP(a0, a1, sv0, sv1, sw_0, sw_1);
+    if (s < S_tot) PF_STEP(a1, a0, sv1, sv0, sw_1, sw_0);
   }
+#undef PF_STEP
+#undef PF_STEP_BODY
+#undef PF_RD_A
+#undef PF_RD_B
+#undef PF_READ
+#undef PF_SW
+#undef PF_DMA_ONE
+#undef PF_DESC
+#undef PF_TABLE
 #undef PF_BROW
 }
 
@@ -332,7 +534,7 @@ int launch_prefill(const PrefillArgs& a, int max_tiles, hipStream_t s) {
   g = (g + 7) / 8 * 8;
   if (g < 8) g = 8;
   MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, grouped_gemm_fp8_prefill_kernel<MODE>,
-             dim3((unsigned)g), dim3(512), 0, s, a);
+             dim3((unsigned)g), dim3(P_THREADS), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -344,6 +546,12 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
                                      const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
                                      const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint8_t* hq,
                                      float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s) {
+  // the DMA takes 32-bit per-lane byte offsets into the activations: rows (<= the sorted
+  // row capacity) x K must stay below 2^32
+  const long max_rows = (long)max_tiles * PBM;
+  if (max_rows * (H > I ? H : I) >= (1L << 32)) return MOE_ERR_INVALID_ARG;
+  // the cross-item DMA pipeline needs at least 4 K blocks per GEMM
+  if (H / PBK < 4 || I / PBK < 4 || H % PBN != 0) return MOE_ERR_INVALID_ARG;
   PrefillArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, nullptr, hq, sh, H, I, k, I / PBK};
   int rc = launch_prefill<PF_GATE_UP>(g1, max_tiles, s);
   if (rc) return rc;

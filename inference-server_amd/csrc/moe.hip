@@ -6,7 +6,7 @@
 // and Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
 #include "common.h"
 
-int moe_gemm_block_m(int S, int E, int H);
+int moe_gemm_block_m(int S, int E, int H, int I);
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
                              const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
@@ -25,9 +25,11 @@ namespace {
 
 // out[t, :] = bf16( sum_j pairs[t*k + j, :] ) with fp32 accumulation in slot order
 // (moe.py:476 view(T,k,H).sum(1)); sentinel slots (ids outside [0,E)) add zero.
+// `wts` (bf16 [T, k]) non-null: the pair rows hold bf16(z) and the routing weight is applied
+// here, bf16(bf16(z) * w), the same rounding as a weighted pair row; null: already weighted.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ pairs, const void* ids,
-                                                      int id_bytes, int T, int k, int H, int E,
-                                                      uint16_t* __restrict__ out) {
+                                                      int id_bytes, const uint16_t* __restrict__ wts, int T,
+                                                      int k, int H, int E, uint16_t* __restrict__ out) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int per_row = H / 8;
   if (idx >= (long)T * per_row) return;
@@ -39,11 +41,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   for (int j0 = 0; j0 < k; j0 += kUnroll) {
     uint4 v[kUnroll];
     bool ok[kUnroll];
+    float wt[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int pr = t * k + min(j0 + u, k - 1);
       const long id = id_bytes == 8 ? (long)((const int64_t*)ids)[pr] : (long)((const int32_t*)ids)[pr];
       ok[u] = j0 + u < k && id >= 0 && id < E;
+      wt[u] = wts ? bf16_to_f32(wts[pr]) : 1.0f;
       v[u] = *(const uint4*)(pairs + (long)pr * H + c8 * 8);
     }
 #pragma unroll
@@ -51,8 +55,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += ok[u] ? __uint_as_float(w[i] << 16) : 0.f;
-        acc[2 * i + 1] += ok[u] ? __uint_as_float(w[i] & 0xffff0000u) : 0.f;
+        float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xffff0000u);
+        if (wts) {
+          lo = round_bf16(lo * wt[u]);
+          hi = round_bf16(hi * wt[u]);
+        }
+        acc[2 * i] += ok[u] ? lo : 0.f;
+        acc[2 * i + 1] += ok[u] ? hi : 0.f;
       }
     }
   }
@@ -86,7 +95,7 @@ struct ExpertsWs {
 ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   ExpertsWs w{};
   const int S = T * k;
-  w.block_m = moe_gemm_block_m(S, E, H);
+  w.block_m = moe_gemm_block_m(S, E, H, I);
   w.max_tiles = moe_mi355x_align_max_tiles(S, E, w.block_m);
   WsCarver c(base);
   w.xq = c.take<uint8_t>((size_t)T * H);
@@ -132,7 +141,8 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
   if (rc) return rc;
   const long threads = (long)T * (H / 8);
   MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     (const uint16_t*)w.pairs, ids, id_bytes, T, k, H, E, (uint16_t*)out);
+                     (const uint16_t*)w.pairs, ids, id_bytes,
+                     w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H, E, (uint16_t*)out);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
