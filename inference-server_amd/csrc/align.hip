@@ -49,16 +49,28 @@ __global__ __launch_bounds__(kChunk) void align_count_kernel(const void* ids, in
 }
 
 // Large S, pass 2 (one workgroup): totals, offsets, tile list, and each chunk's
-// starting slot per expert, written back over bc.
+// starting slot per expert, written back over bc.  The chunk histograms are staged in
+// LDS when they fit (every per-expert walk over the chunks then reads LDS, not global
+// memory with one round trip per chunk).
+constexpr int kScanLds = 16384;  // ints of staged histograms (64 KB)
 __global__ __launch_bounds__(kChunk) void align_scan_kernel(int32_t* bc, int nb, int E, int block_m,
                                                             int32_t* counts, int32_t* offsets, int32_t* tiles,
                                                             int32_t* n_tiles) {
   __shared__ int s_cnt[kBuckets];
   __shared__ int s_off[kBuckets];
   __shared__ int s_toff[kBuckets];
+  __shared__ int s_bc[kScanLds];
+  const int n = nb * (E + 1);
+  const bool staged = n <= kScanLds;  // workgroup-uniform
+  if (staged) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s_bc[i] = bc[i];
+    __syncthreads();
+  }
+  const int32_t* src = staged ? s_bc : bc;
   for (int e = threadIdx.x; e <= E; e += blockDim.x) {
     int tot = 0;
-    for (int b = 0; b < nb; ++b) tot += bc[(long)b * (E + 1) + e];
+#pragma unroll 8
+    for (int b = 0; b < nb; ++b) tot += src[(long)b * (E + 1) + e];
     s_cnt[e] = tot;
   }
   __syncthreads();
@@ -67,8 +79,9 @@ __global__ __launch_bounds__(kChunk) void align_scan_kernel(int32_t* bc, int nb,
   emit_meta(s_cnt, s_off, s_toff, E, block_m, counts, offsets, tiles, n_tiles);
   for (int e = threadIdx.x; e <= E; e += blockDim.x) {
     int run = s_off[e];
+#pragma unroll 8
     for (int b = 0; b < nb; ++b) {
-      const int c = bc[(long)b * (E + 1) + e];
+      const int c = src[(long)b * (E + 1) + e];
       bc[(long)b * (E + 1) + e] = run;
       run += c;
     }

@@ -38,16 +38,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   // rows are loaded unconditionally (a sentinel slot's row exists, unwritten) and masked
   // afterwards, so that the k loads are in flight together rather than one per branch
   constexpr int kUnroll = 8;
+  // eight weights of a token in one 16-byte load when the rows allow it
+  const bool wvec = wts != nullptr && (k & 7) == 0 && ((uintptr_t)wts & 15) == 0;
   for (int j0 = 0; j0 < k; j0 += kUnroll) {
     uint4 v[kUnroll];
     bool ok[kUnroll];
     float wt[kUnroll];
+    if (wvec) {
+      const uint4 w8 = *(const uint4*)(wts + (long)t * k + j0);
+      const uint32_t ww[4] = {w8.x, w8.y, w8.z, w8.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wt[2 * i] = __uint_as_float(ww[i] << 16);
+        wt[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int pr = t * k + min(j0 + u, k - 1);
       const long id = id_bytes == 8 ? (long)((const int64_t*)ids)[pr] : (long)((const int32_t*)ids)[pr];
       ok[u] = j0 + u < k && id >= 0 && id < E;
-      wt[u] = wts ? bf16_to_f32(wts[pr]) : 1.0f;
+      if (!wvec) wt[u] = wts ? bf16_to_f32(wts[pr]) : 1.0f;
       v[u] = *(const uint4*)(pairs + (long)pr * H + c8 * 8);
     }
 #pragma unroll

@@ -12,9 +12,14 @@ constexpr int kRouterBlockE = 64;   // experts per workgroup (4 waves)
 constexpr int kMaxKSplit = 16;      // router K-split partials summed by the top-k kernel
 
 // partial[z, t, e] = sum over k in chunk z of x[t, k] * w[e, k]   (fp32)
-// grid (ceil(T/16), ceil(E/64), ksplit), block 256.  With xq != nullptr the workgroups
-// of expert block 0 also quantise their 16 x kchunk slice of x (kchunk % 128 == 0), so
-// the experts need no separate activation-quantisation pass.
+// grid (ceil(T/16), ceil(E/64), ksplit), block 256: wave w computes tokens t0..t0+15 x
+// experts e0 + 16 w ..  Each 128-wide K chunk is loaded one chunk ahead of its MFMAs (two
+// register sets), so a wave keeps a chunk of loads in flight instead of paying one load
+// round trip per chunk.  With xq != nullptr the workgroups of expert block 0 also quantise
+// the x rows they load (kchunk % 128 == 0): lane (r, g) holds 8 bf16 at columns
+// k + 32 u + 8 g of row r for u = 0..3, i.e. the four lanes r, r+16, r+32, r+48 hold one
+// complete 128-column group; every wave forms the group amax and wave w quantises and
+// stores the values of u = w.
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wr, int T, int H,
                                                           int E, int kchunk, float* __restrict__ part,
@@ -23,48 +28,186 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
   const int t0 = blockIdx.x * kRouterTileT;
   const int kbeg = blockIdx.z * kchunk;
   const int kend = min(H, kbeg + kchunk);
-  if (xq != nullptr && blockIdx.y == 0) {
-    const int groups = kRouterTileT * ((kend - kbeg) / MOE_GROUP);
-    const int sub = threadIdx.x & 15;
-    for (int g = threadIdx.x >> 4; g < groups; g += 16) {
-      const int t = t0 + g % kRouterTileT;
-      const int k0 = kbeg + (g / kRouterTileT) * MOE_GROUP;
-      if (t < T) {  // the 16 lanes of a group share t
-        const long elem = (long)t * H + k0 + sub * 8;
-        quant_group16(x + elem, xq + elem, sx + (long)t * (H / MOE_GROUP) + k0 / MOE_GROUP, sub);
-      }
-    }
-  }
-  const int e0 = blockIdx.y * kRouterBlockE + wave * kRouterWaveE;
-  if (e0 >= E) return;  // wave-uniform
+  const bool quant = xq != nullptr && blockIdx.y == 0;  // workgroup-uniform
+  const int e0 = min(blockIdx.y * kRouterBlockE + wave * kRouterWaveE, E - 1);
   const int rt = min(t0 + (lane & 15), T - 1);  // clamped rows compute garbage that is never stored
   const int re = min(e0 + (lane & 15), E - 1);
   const int kq = (lane >> 4) * 8;
   const uint16_t* xa = x + (long)rt * H + kq;
   const uint16_t* wb = wr + (long)re * H + kq;
+  const bool row_ok = t0 + (lane & 15) < T;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
-  int k = kbeg;
-  for (; k + 128 <= kend; k += 128) {
-    v8bf a[4], b[4];
+  const int n128 = (kend - kbeg) >> 7;  // whole 128-wide chunks
+  v8bf a0[4], b0[4], a1[4], b1[4];
+  // MFMAs of chunk c_ on (A_, B_) after issuing the loads of chunk c_ + 1 (clamped: the
+  // last chunk reloads itself) into (AN_, BN_), then the x quantisation of chunk c_
+#define ROUTER_STEP(A_, B_, AN_, BN_, c_)                                                         \
+  do {                                                                                            \
+    const int kk_ = kbeg + 128 * (c_);                                                            \
+    const int nx_ = kbeg + 128 * min((c_) + 1, n128 - 1);                                         \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                               \
+      AN_[u] = *(const v8bf*)(xa + nx_ + 32 * u);                                                 \
+      BN_[u] = *(const v8bf*)(wb + nx_ + 32 * u);                                                 \
+    }                                                                                             \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A_[u], B_[u], acc, 0, 0, 0); \
+    if (quant) {                                                                                  \
+      /* the e4m3 rule of quant_group16: s = amax / 448 (1 if 0), q = e4m3(clamp(x / s)) */      \
+      float amax = 0.f;                                                                           \
+      _Pragma("unroll") for (int u = 0; u < 4; ++u)                                               \
+        _Pragma("unroll") for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf((float)A_[u][i])); \
+      amax = fmaxf(amax, __shfl_xor(amax, 16));                                                   \
+      amax = fmaxf(amax, __shfl_xor(amax, 32));                                                   \
+      const float sc = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;                                    \
+      const v8bf av = wave == 0 ? A_[0] : wave == 1 ? A_[1] : wave == 2 ? A_[2] : A_[3];         \
+      float v[8];                                                                                 \
+      _Pragma("unroll") for (int i = 0; i < 8; ++i) v[i] = (float)av[i];                          \
+      uint2 o;                                                                                    \
+      o.x = pack4_e4m3(clamp_fp8(v[0] / sc), clamp_fp8(v[1] / sc), clamp_fp8(v[2] / sc), clamp_fp8(v[3] / sc)); \
+      o.y = pack4_e4m3(clamp_fp8(v[4] / sc), clamp_fp8(v[5] / sc), clamp_fp8(v[6] / sc), clamp_fp8(v[7] / sc)); \
+      if (row_ok) {                                                                               \
+        const long row = t0 + (lane & 15);                                                        \
+        *(uint2*)(xq + row * H + kk_ + 32 * wave + kq) = o;                                       \
+        if (wave == 0 && kq == 0) sx[row * (H / MOE_GROUP) + kk_ / MOE_GROUP] = sc;               \
+      }                                                                                           \
+    }                                                                                             \
+  } while (0)
+  if (n128 > 0) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      a[u] = *(const v8bf*)(xa + k + 32 * u);
-      b[u] = *(const v8bf*)(wb + k + 32 * u);
+      a0[u] = *(const v8bf*)(xa + kbeg + 32 * u);
+      b0[u] = *(const v8bf*)(wb + kbeg + 32 * u);
     }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u], b[u], acc, 0, 0, 0);
   }
+  for (int c = 0; c < n128; c += 2) {
+    ROUTER_STEP(a0, b0, a1, b1, c);
+    if (c + 1 < n128) ROUTER_STEP(a1, b1, a0, b0, c + 1);
+  }
+#undef ROUTER_STEP
+  int k = kbeg + 128 * n128;
   for (; k < kend; k += 32) {
     v8bf a = *(const v8bf*)(xa + k), b = *(const v8bf*)(wb + k);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
   }
   // D[i][j] lives in lane j + 16*(i/4), element i%4; i = token, j = expert.
-  const int e = e0 + (lane & 15);
+  const int e = blockIdx.y * kRouterBlockE + wave * kRouterWaveE + (lane & 15);
   if (e >= E) return;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = t0 + 4 * (lane >> 4) + r;
     if (t < T) part[((long)blockIdx.z * T + t) * E + e] = acc[r];
+  }
+}
+
+// Router GEMM for large batches: workgroup tile 64 tokens x 128 experts, K in 128-wide
+// chunks staged through LDS (x 16 KB, W 32 KB per chunk), so each x row and each router row
+// is read once per workgroup instead of once per wave.  Wave w computes tokens 16w..16w+15
+// against all 128 experts (8 MFMA tiles).  The next chunk is loaded into registers while the
+// current one is computed.  LDS rows are 256 bytes (16 chunks of 8 bf16); chunk c of row r
+// is stored at c ^ (r & 15), so the 16 rows of an MFMA fragment read hit 16 distinct bank
+// groups.  With xq != nullptr the workgroups of expert block 0 quantise the staged x chunk:
+// the four lanes r, r+16, r+32, r+48 of wave w hold row 16w + r's 128-column group.
+constexpr int kRtT = 64, kRtE = 128;
+__global__ __launch_bounds__(256) void router_gemm_tiled_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ wr, int T, int H,
+                                                                int E, int kchunk, float* __restrict__ part,
+                                                                uint8_t* __restrict__ xq, float* __restrict__ sx) {
+  __shared__ uint4 s_x[kRtT * 16];
+  __shared__ uint4 s_w[kRtE * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int t0 = blockIdx.x * kRtT, eb = blockIdx.y * kRtE;
+  const int kbeg = blockIdx.z * kchunk;
+  const int nch = (min(H, kbeg + kchunk) - kbeg) >> 7;  // kchunk is a multiple of 128 here
+  const bool quant = xq != nullptr && blockIdx.y == 0;
+  // loader: x tile 64 rows x 16 chunks (4 per thread), W tile 128 x 16 (8 per thread)
+  uint4 xr0, xr1, xr2, xr3, wv0, wv1, wv2, wv3, wv4, wv5, wv6, wv7;
+#define RT_LD(dst_, base_, rowbase_, rowmax_, i_)                                                 \
+  do {                                                                                            \
+    const int idx_ = tid + 256 * (i_);                                                            \
+    dst_ = *(const uint4*)((base_) + (long)min((rowbase_) + (idx_ >> 4), (rowmax_)) * H + k0_ + 8 * (idx_ & 15)); \
+  } while (0)
+#define RT_LOAD(c_)                                                                               \
+  do {                                                                                            \
+    const int k0_ = kbeg + 128 * (c_);                                                            \
+    RT_LD(xr0, x, t0, T - 1, 0); RT_LD(xr1, x, t0, T - 1, 1); RT_LD(xr2, x, t0, T - 1, 2); RT_LD(xr3, x, t0, T - 1, 3); \
+    RT_LD(wv0, wr, eb, E - 1, 0); RT_LD(wv1, wr, eb, E - 1, 1); RT_LD(wv2, wr, eb, E - 1, 2); RT_LD(wv3, wr, eb, E - 1, 3); \
+    RT_LD(wv4, wr, eb, E - 1, 4); RT_LD(wv5, wr, eb, E - 1, 5); RT_LD(wv6, wr, eb, E - 1, 6); RT_LD(wv7, wr, eb, E - 1, 7); \
+  } while (0)
+#define RT_ST(arr_, v_, i_)                                                                       \
+  do {                                                                                            \
+    const int idx_ = tid + 256 * (i_), row_ = idx_ >> 4;                                          \
+    arr_[row_ * 16 + ((idx_ & 15) ^ (row_ & 15))] = v_;                                           \
+  } while (0)
+  RT_LOAD(0);
+  v4f acc[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nch; ++c) {
+    __syncthreads();  // the previous chunk's readers are done
+    RT_ST(s_x, xr0, 0); RT_ST(s_x, xr1, 1); RT_ST(s_x, xr2, 2); RT_ST(s_x, xr3, 3);
+    RT_ST(s_w, wv0, 0); RT_ST(s_w, wv1, 1); RT_ST(s_w, wv2, 2); RT_ST(s_w, wv3, 3);
+    RT_ST(s_w, wv4, 4); RT_ST(s_w, wv5, 5); RT_ST(s_w, wv6, 6); RT_ST(s_w, wv7, 7);
+    __syncthreads();
+    RT_LOAD(min(c + 1, nch - 1));  // the last chunk reloads itself (no branch around the loads)
+    const int arow = 16 * wave + lr;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int ch = 4 * k4 + lg;
+      const v8bf a = __builtin_bit_cast(v8bf, s_x[arow * 16 + (ch ^ lr)]);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const v8bf b = __builtin_bit_cast(v8bf, s_w[(16 * n + lr) * 16 + (ch ^ lr)]);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[n], 0, 0, 0);
+      }
+    }
+    if (quant) {
+      // the e4m3 rule of quant_group16: s = amax / 448 (1 if 0), q = e4m3(clamp(x / s));
+      // lane (r, g) holds chunks 4g..4g+3 of row 16w + r
+      float v[32];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ch = 4 * lg + i;
+        const uint4 q = s_x[arow * 16 + (ch ^ lr)];
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          v[8 * i + 2 * h] = __uint_as_float(w4[h] << 16);
+          v[8 * i + 2 * h + 1] = __uint_as_float(w4[h] & 0xffff0000u);
+        }
+      }
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      const float sc = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
+      uint32_t o[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        o[i] = pack4_e4m3(clamp_fp8(v[4 * i] / sc), clamp_fp8(v[4 * i + 1] / sc), clamp_fp8(v[4 * i + 2] / sc),
+                          clamp_fp8(v[4 * i + 3] / sc));
+      const int t = t0 + arow;
+      if (t < T) {
+        uint8_t* dst = xq + (long)t * H + kbeg + 128 * c + 32 * lg;
+        *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+        *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+        if (lg == 0) sx[(long)t * (H / MOE_GROUP) + (kbeg >> 7) + c] = sc;
+      }
+    }
+  }
+#undef RT_LOAD
+#undef RT_LD
+#undef RT_ST
+  // D[i][j] lives in lane j + 16*(i/4), element i%4; i = token, j = expert.
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    const int e = eb + 16 * n + lr;
+    if (e >= E) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 16 * wave + 4 * lg + r;
+      if (t < T) part[((long)blockIdx.z * T + t) * E + e] = acc[n][r];
+    }
   }
 }
 
@@ -230,7 +373,17 @@ __global__ __launch_bounds__(kChunk) void topk_align_kernel(const float* __restr
   for (int c0 = 0; c0 < S; c0 += kChunk) scatter_chunk(s_ids, 4, S, E, c0, s_off, s_wcnt, perm);
 }
 
+// Large batches use the LDS-tiled router GEMM (one tile per 64 tokens x 128 experts).
+bool route_tiled(int T, int H) { return T >= 512 && H % 128 == 0; }
+
 int route_ksplit(int T, int H, int E) {
+  if (route_tiled(T, H)) {
+    // about two workgroups per CU; K chunks of at least 256
+    const int tiles = ((T + kRtT - 1) / kRtT) * ((E + kRtE - 1) / kRtE);
+    int ks = (512 + tiles - 1) / tiles;
+    const int kmax = H / 256 > 0 ? (H / 256 < kMaxKSplit ? H / 256 : kMaxKSplit) : 1;
+    return ks < 1 ? 1 : (ks > kmax ? kmax : ks);
+  }
   const int tiles = ((T + kRouterTileT - 1) / kRouterTileT) * ((E + kRouterBlockE - 1) / kRouterBlockE);
   int ks = (256 + tiles - 1) / tiles;
   int kmax = H / 256 > 0 ? H / 256 : 1;
@@ -279,13 +432,20 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   MOE_RETURN_IF(quant && H % MOE_GROUP, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(perm != nullptr && !moe_route_can_fuse_align(T, E, k), MOE_ERR_INVALID_ARG);
   const int ks = route_ksplit(T, H, E);
-  const int kchunk = route_kchunk(H, ks, quant);
+  const bool tiled = route_tiled(T, H);
+  const int kchunk = route_kchunk(H, ks, quant || tiled);
   const int ks_eff = (H + kchunk - 1) / kchunk;  // <= ks: the workspace holds ks partial slabs
   MOE_RETURN_IF(workspace_bytes < moe_mi355x_route_workspace_bytes(T, H, E) || !workspace, MOE_ERR_WORKSPACE);
   float* part = (float*)workspace;
-  dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
-  MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
-             (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx);
+  if (tiled) {
+    dim3 g1((T + kRtT - 1) / kRtT, (E + kRtE - 1) / kRtE, ks_eff);
+    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_tiled_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx);
+  } else {
+    dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
+    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx);
+  }
   MOE_CHECK_LAUNCH();
   if (perm != nullptr) {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_align_kernel, dim3(1), dim3(kChunk), 0, s, part, ks_eff, T, E, k, renorm,

@@ -291,3 +291,15 @@ def test_sentinel_pairs_contribute_zero(pkg, dev, w30b):
     ref = pkg.experts_fp8(to_bf16(x, dev), to_dev(ids0, dev), to_bf16(w0, dev), *w30b)
     max_abs, _ = errors(np_f32(out), np_f32(ref))
     assert max_abs <= 1e-2
+
+
+@pytest.mark.parametrize("T", [8, 64, 600, 1024])
+def test_block_fused_quant_is_bit_exact(pkg, dev, w30b, router30b, T):
+    """The block path quantises x inside the router GEMM; the experts path quantises it in
+    its own kernel.  Fed the block's routing, the experts path must reproduce the block's
+    output bit for bit (same e4m3 codes and scales, same deterministic GEMMs)."""
+    rng = np.random.default_rng(70 + T)
+    x = to_bf16(orc.gen_normal_bf16(rng, (T, 2048)), dev)
+    out, (_, w, ids) = pkg.moe_block_fp8(x, router30b, 8, *w30b, return_routing=True)
+    ref = pkg.experts_fp8(x, ids, w, *w30b)
+    assert torch.equal(out, ref)
