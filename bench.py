@@ -11,10 +11,11 @@ Weights are rotated over enough copies that one step's weights never sit in the 
 last-level cache from an earlier step; inputs rotate too, so routing changes every step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--zipf] [--no-sweep]
-                       [--no-cpu] [--copy-probe]
+                       [--no-cpu] [--copy-probe] [--shape 30b|235b]
   --zipf        apply the calibrated Zipf(s=1.1) router bias to the headline batch (config 3)
   --copy-probe  first run a plain 256 MiB device copy three times: the reference kernel whose
                 FETCH_SIZE / WRITE_SIZE counters calibrate the traffic measurement
+  --shape 235b  the headline line on the Qwen3-235B-A22B layer instead (with --no-sweep, for profiling)
 """
 
 from __future__ import annotations
@@ -291,6 +292,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--zipf", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--shape", choices=["30b", "235b"], default="30b",
+                    help="layer of the headline line: Qwen3-30B-A3B (default) or Qwen3-235B-A22B")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (expert-parallel sharding "
@@ -312,7 +315,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    layer = Layer(pkg, torch, dev, S30B, n_copies=16)
+    layer = Layer(pkg, torch, dev, S30B, n_copies=16) if args.shape == "30b" else Layer(pkg, torch, dev, S235B, n_copies=2)
     shape = layer.shape
 
     T = args.tokens
