@@ -81,6 +81,17 @@ class Shape:
 S30B = Shape("qwen3-30b-a3b", 2048, 768)
 S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 
+# HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script
+# (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy):
+#   decode 64:            rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} ... -- python3 bench.py --no-sweep --no-cpu
+#                         --steps 10 --warmup 2 --copy-probe           -> 193,412 / 920 KiB
+#   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
+#                         --copy-probe                                 -> 291,674 / 25,447 KiB
+MEASURED_GATE_UP_TRAFFIC = {
+    ("qwen3-30b-a3b", 64): 193412 * 1024 * 2 + 920 * 1024,
+    ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
+}
+
 
 class Layer:
     """Router + FP8 experts of one shape, with `n_copies` distinct copies of the experts."""
@@ -212,16 +223,17 @@ def roofline_for(shape, T, slots, n_active):
     """Roofline of the dominant kernel, gate_up: HBM-bound on the decode path (bytes of the
     measured active experts), MFMA-bound on the 128-row prefill path."""
     dur_ms = slots["gemm_gate_up"]
+    traffic = MEASURED_GATE_UP_TRAFFIC.get((shape.name, T))
     if shape.prefill_path(T):
         flops = shape.gate_up_flops(T)
         achieved = flops / dur_ms / 1e9  # TFLOP/s
         return {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
                 "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                "traffic": None, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+                "traffic": traffic, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
     byts = shape.gate_up_bytes(n_active, T)
     achieved = byts / (dur_ms * 1e-3) / 1e9  # GB/s
     return {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
 
 
