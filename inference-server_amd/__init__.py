@@ -6,16 +6,20 @@ Importable as ``inference_server_amd`` (the on-disk folder name carries a hyphen
 Layers:
   ``_lib``     ctypes binding of ``libmoe_mi355x.so`` (C ABI: ``include/moe_mi355x.h``)
   ``kernels``  torch-tensor wrappers of every entry point
-  ``experts``  drop-in modules and the transformers experts-interface registration
+  ``experts``  drop-in modules, the transformers experts-interface registration, and the
+               HIP-graph replay of a block per decode batch bucket
+  ``checkpoint`` FP8 expert layers from a local safetensors checkpoint
   ``build``    hipcc build of the library
 """
 
 from __future__ import annotations
 
 from . import _lib, kernels  # noqa: F401
+from .checkpoint import CheckpointIndex, load_moe_block, load_moe_layer  # noqa: F401
 from .experts import (  # noqa: F401
     IMPLEMENTATION_KEY,
     MI355XFp8Experts,
+    MI355XGraphedMoeBlock,
     MI355XSparseMoeBlock,
     MI355XTopKRouter,
     mi355x_fp8_experts_forward,

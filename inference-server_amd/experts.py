@@ -176,3 +176,67 @@ def swap_moe_blocks(model: nn.Module) -> int:
         parent = model.get_submodule(parent_name) if parent_name else model
         setattr(parent, child, MI355XSparseMoeBlock.from_hf_block(mod))
     return len(targets)
+
+
+class MI355XGraphedMoeBlock(nn.Module):
+    """HIP-graph replay of an ``MI355XSparseMoeBlock`` per decode batch bucket.
+
+    The reference's decode step runs the whole batch through the model once per scheduler
+    iteration (scheduler.py:379-402, torch_backend.py:305-322); at small batches the launch chain,
+    not the weight stream, sets the MoE layer's time.  This wrapper captures the block's launches
+    once per bucket size (the smallest bucket >= the batch; batches are zero-padded up to it, and
+    the padded rows' outputs are dropped) and replays the graph afterwards.  Batches above the
+    largest bucket run eagerly.  Inputs are copied into the graph's static buffer, so the caller's
+    tensors may live anywhere.  Graphs are captured on first use of a bucket; ``capture()``
+    captures them up front.
+    """
+
+    def __init__(self, block: MI355XSparseMoeBlock, buckets=(1, 2, 4, 8, 16, 32, 64, 128, 256)):
+        super().__init__()
+        self.block = block
+        self.buckets = tuple(sorted(set(int(b) for b in buckets)))
+        self._graphs: dict[int, tuple] = {}
+
+    def _bucket(self, t: int) -> int | None:
+        for b in self.buckets:
+            if b >= t:
+                return b
+        return None
+
+    def capture(self, buckets=None) -> None:
+        for b in buckets or self.buckets:
+            self._graph(b)
+
+    def _graph(self, b: int):
+        g = self._graphs.get(b)
+        if g is not None:
+            return g
+        H = self.block.gate.hidden_dim
+        dev = self.block.gate.weight.device
+        x_static = torch.zeros((b, H), dtype=torch.bfloat16, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # warm the allocator for the capture stream
+            self.block(x_static)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out_static = self.block(x_static)
+        g = (graph, x_static, out_static)
+        self._graphs[b] = g
+        return g
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        shape = hidden_states.shape
+        x = hidden_states.reshape(-1, shape[-1])
+        t = x.shape[0]
+        b = self._bucket(t)
+        if b is None or t == 0:
+            return self.block(hidden_states)
+        graph, x_static, out_static = self._graph(b)
+        x_static[:t].copy_(x)
+        if t < b:
+            x_static[t:].zero_()
+        graph.replay()
+        return out_static[:t].to(hidden_states.dtype).reshape(shape)
