@@ -210,10 +210,13 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
                                      const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint8_t* hq,
                                      float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s);
 
-// Tile height (rows per M tile) for S pairs over E experts: 16-row tiles stream weights
-// (decode); 128-row tiles go to the LDS-tiled MFMA kernel (prefill, needs H % 256 == 0).
+// Tile height (rows per M tile) for S pairs over E experts: 16- or 32-row tiles stream
+// weights (decode); 128-row tiles go to the LDS-tiled MFMA kernel (prefill, needs H % 256 == 0).
 int moe_gemm_block_m(int S, int E, int H, int I) {
-  if (S <= 16 * E) return 16;
+  if (S <= 8 * E) return 16;
+  // beyond 8 pairs per expert on average, 16-row tiles would split many experts in two and
+  // stream their weights twice: 32-row tiles keep one tile per expert for the usual loads
+  if (S <= 16 * E) return 32;
   // the 128-row prefill path: 256-column tiles of H, and at least 4 K blocks in each GEMM
   // for its cross-item DMA pipeline
   return H % 256 == 0 && H >= 512 && I >= 512 ? 128 : 64;
@@ -231,6 +234,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   int rc;
   if (block_m == 16)
     rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
+  else if (block_m == 32)
+    rc = launch_gemm<MODE_GATE_UP, 2, 4>(g1, max_tiles, s);
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
@@ -241,6 +246,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
   if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
     rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  else if (block_m == 32)
+    rc = launch_gemm<MODE_DOWN, 2, 2, 2>(g2, max_tiles, s);
   else
     rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
   return rc;
