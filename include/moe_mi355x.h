@@ -127,6 +127,36 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
                          void* weights, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Paged GQA decode attention, one new token per sequence (the attention of a decode step of
+ * Qwen3MoeAttention.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:151-191, with
+ * eager_attention_forward :96-119): for query head h of sequence b, over the keys
+ * 0 .. context_lens[b]-1 of kv head h / (Hq / Hkv):
+ *   s = bf16(bf16(q . k) * scale),  out = bf16( softmax_fp32(s) . V )
+ * (the softmax is applied unnormalised and divided once, in fp32).
+ *   q            bf16 [B, Hq, 128]          out bf16 [B, Hq, 128]
+ *   k_cache      bf16 [pages, Hkv, 16, 128] (token rows)
+ *   v_cache      bf16 [pages, Hkv, 128, 16] (transposed: dim rows)
+ *   block_tables int32 [B, max_pages]       page of each 16-token block of a sequence
+ *   context_lens int32 [B]                  >= 1, <= 16 * max_pages
+ * The KV layout is this library's; the reference keeps a contiguous per-layer cache.
+ * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16.
+ */
+size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages);
+int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* block_tables, const int32_t* context_lens, int B, int Hq,
+                                 int Hkv, int head_dim, int page_size, int max_pages, float scale, void* out,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * KV-cache append of one token per sequence at position positions[b] (the cache update of
+ * Qwen3MoeAttention.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:170-171, in the paged
+ * layout above).  k, v: bf16 [B, Hkv, 128] (k after k_norm and rotary embedding).
+ */
+int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
+                         const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
+                         int head_dim, int page_size, int max_pages, void* stream);
+
+/*
  * Kernel timing (instrumentation; no counterpart in the reference).  While enabled, each
  * kernel launch of this library is bracketed by hipEvents on its stream; profile_read
  * waits for them and returns the launch count and summed duration (ms) of one slot:

@@ -29,7 +29,9 @@ from .experts import (  # noqa: F401
 from .kernels import (  # noqa: F401
     align,
     experts_fp8,
+    kv_append,
     moe_block_fp8,
+    paged_attention_decode,
     quantize_act_fp8,
     quantize_weight_fp8,
     route,

@@ -1,0 +1,301 @@
+// Paged GQA decode attention (one new token per sequence) for the Qwen3-MoE decoder layer,
+// bf16 in and out, fp32 softmax and accumulation.
+//
+// Reference: eager_attention_forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:96-119, as
+// called by Qwen3MoeAttention.forward (:151-191) for a decode step: scores
+// bf16(bf16(q . k) * head_dim^-0.5), softmax in fp32 over the keys of the sequence, the
+// probabilities applied to V, output bf16.  The grouped-query heads share a key/value head
+// (repeat_kv, :84-93): query head h reads key/value head h / (Hq / Hkv).
+//
+// KV cache (this library's layout; the reference keeps a contiguous per-layer cache): pages
+// of 16 tokens.  K pages are [page][kv head][token 16][dim 128] and V pages are stored
+// transposed, [page][kv head][dim 128][token 16], so that both MFMA products below take
+// their operands straight from HBM with 16- and 8-byte loads.
+//
+// One workgroup = (sequence b, kv head g, split of up to `pps` pages); its 4 waves take the
+// split's pages round robin, each with its own online-softmax state, merged in LDS at the
+// end.  Per page a wave computes
+//   S^T [16 keys x 16 heads] = K [16 x 128] . Q^T [128 x 16]     (4 x mfma 16x16x32 bf16)
+//   O   [16 heads x 128]    += P [16 x 16 keys] . V [16 keys x 128] (8 x mfma 16x16x16 bf16)
+// where the query heads of the group fill rows 0..G-1 (G <= 16) and the rest are zero.  The
+// score tile's lane layout (lane l: keys 4 (l >> 4) + i of head l & 15) is exactly the A
+// operand layout of the second product, so P needs no shuffle.  Splits are combined by
+// paged_attn_merge_kernel (log-sum-exp weights).
+#include "common.h"
+
+namespace {
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+constexpr int kHD = 128;        // head dim
+constexpr int kPage = 16;       // tokens per page
+constexpr int kAttnWaves = 4;
+
+__device__ __forceinline__ float bf16_round(float f) { return (float)(__bf16)f; }
+
+struct AttnArgs {
+  const uint16_t* q;           // [B, Hq, 128] bf16
+  const uint16_t* k_cache;     // [pages, Hkv, 16, 128] bf16
+  const uint16_t* v_cache;     // [pages, Hkv, 128, 16] bf16
+  const int32_t* block_tables; // [B, max_pages]
+  const int32_t* context_lens; // [B]
+  float* part_o;               // [B, Hkv, max_splits, G, 128] unnormalised outputs
+  float* part_ml;              // [B, Hkv, max_splits, G, 2] (running max, sum)
+  int Hq, Hkv, max_pages, max_splits, pps;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void paged_attn_decode_kernel(AttnArgs a) {
+  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int G = a.Hq / a.Hkv;
+  const int ctx = a.context_lens[b];
+  const int n_pages = (ctx + kPage - 1) / kPage;
+  const int p_begin = split * a.pps;
+  if (p_begin >= n_pages) return;  // workgroup-uniform
+  const int p_end = min(n_pages, p_begin + a.pps);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // Q^T operand (B of the score product): head lr of the group, dims 32 kk + 8 lg .. +8
+  v8bf qop[4];
+  {
+    const bool live = lr < G;
+    const uint16_t* qrow = a.q + ((long)b * a.Hq + g * G + (live ? lr : 0)) * kHD;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint4 v = live ? *(const uint4*)(qrow + 32 * kk + 8 * lg) : make_uint4(0, 0, 0, 0);
+      qop[kk] = __builtin_bit_cast(v8bf, v);
+    }
+  }
+
+  const int32_t* btab = a.block_tables + (long)b * a.max_pages;
+  const long kv_head_stride = (long)kHD * kPage;  // elements per (page, kv head)
+
+  float m_run = -INFINITY, l_run = 0.f;  // of head lr (identical in the 4 lanes lr + 16 j)
+  v4f o[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) o[n] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  // operands of one page: K rows (lane: key lr, dims 32 kk + 8 lg) and V^T (lane: keys
+  // 4 lg .. +4 of dim 16 n + lr)
+  uint4 kr[4];
+  uint2 vr[8];
+  auto load_page = [&](int p) __attribute__((always_inline)) {
+    const long pg = btab[p];
+    const uint16_t* kb = a.k_cache + (pg * a.Hkv + g) * kv_head_stride;
+    const uint16_t* vb = a.v_cache + (pg * a.Hkv + g) * kv_head_stride;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kr[kk] = *(const uint4*)(kb + lr * kHD + 32 * kk + 8 * lg);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) vr[n] = *(const uint2*)(vb + (16 * n + lr) * kPage + 4 * lg);
+  };
+
+  int p = p_begin + wave;
+  if (p < p_end) load_page(p);
+  for (; p < p_end; p += kAttnWaves) {
+    uint4 kc[4];
+    uint2 vc[8];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kc[kk] = kr[kk];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) vc[n] = vr[n];
+    if (p + kAttnWaves < p_end) load_page(p + kAttnWaves);  // next page of this wave in flight
+
+    // scores S^T: lane holds keys 4 lg + i of head lr
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kc[kk]), qop[kk], s, 0, 0, 0);
+    const int key0 = p * kPage + 4 * lg;
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the reference's rounding: bf16 matmul output, then a bf16 multiply by the scale
+      const float x = bf16_round(bf16_round(s[i]) * a.scale);
+      sv[i] = key0 + i < ctx ? x : -INFINITY;
+    }
+    float pm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    pm = fmaxf(pm, __shfl_xor(pm, 16));
+    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    const float m_new = fmaxf(m_run, pm);  // finite: every page has at least one live key
+    const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * 1.4426950408889634f);  // 0 on the first page
+    float pv[4], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pv[i] = __builtin_amdgcn_exp2f((sv[i] - m_new) * 1.4426950408889634f);
+      ps += pv[i];
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * corr + ps;
+    m_run = m_new;
+    // P as the A operand (head lr, keys 4 lg + i)
+    v4s pa;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pa[i] = (short)f32_to_bf16(pv[i]);
+    // rows of O in this lane are heads 4 lg + i: their correction factors live in lanes 4 lg + i
+    float cr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * lg + i);
+    // keys past the end of the sequence (last page) have P = 0; their V slots may hold
+    // anything (the pool is not cleared), so they are zeroed rather than multiplied by 0
+    const int live_keys = ctx - key0;  // keys 4 lg + j with j < live_keys are valid
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      uint2 v = vc[n];
+      if (live_keys < 4) {
+        if (live_keys <= 0) v.x = v.y = 0u;
+        else if (live_keys == 1) { v.x &= 0xffffu; v.y = 0u; }
+        else if (live_keys == 2) v.y = 0u;
+        else v.y &= 0xffffu;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[n][i] *= cr[i];
+      v4s vb;
+      vb[0] = (short)(v.x & 0xffffu);
+      vb[1] = (short)(v.x >> 16);
+      vb[2] = (short)(v.y & 0xffffu);
+      vb[3] = (short)(v.y >> 16);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[n], 0, 0, 0);
+    }
+  }
+
+  // merge the 4 waves: per head max, sum and O rows (heads 4 lg + i, dims 16 n + lr)
+  __shared__ float s_m[kAttnWaves][16], s_l[kAttnWaves][16];
+  __shared__ float s_o[kAttnWaves][16][kHD + 4];
+  if (lg == 0) {
+    s_m[wave][lr] = m_run;
+    s_l[wave][lr] = l_run;
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_o[wave][4 * lg + i][16 * n + lr] = o[n][i];
+  __syncthreads();
+  // 256 threads: head hh = tid / 16 (< G used), dims 8 (tid % 16) .. +8
+  const int hh = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
+  if (hh < G) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, s_m[w][hh]);
+    float wgt[kAttnWaves], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      // a wave with no pages in this split has m = -inf and contributes nothing
+      wgt[w] = s_m[w][hh] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((s_m[w][hh] - M) * 1.4426950408889634f);
+      L += s_l[w][hh] * wgt[w];
+    }
+    const long base = (((long)b * a.Hkv + g) * a.max_splits + split) * G + hh;
+    float* dst = a.part_o + base * kHD + d0;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) acc += s_o[w][hh][d0 + d] * wgt[w];
+      dst[d] = acc;
+    }
+    if ((threadIdx.x & 15) == 0) {
+      a.part_ml[base * 2] = M;
+      a.part_ml[base * 2 + 1] = L;
+    }
+  }
+}
+
+// out[b, h, :] = bf16( sum_s w_s O_s / sum_s w_s l_s ), w_s = exp(m_s - max m)
+__global__ __launch_bounds__(128) void paged_attn_merge_kernel(AttnArgs a, uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int G = a.Hq / a.Hkv, g = h / G, hh = h % G;
+  const int n_pages = (a.context_lens[b] + kPage - 1) / kPage;
+  const int ns = (n_pages + a.pps - 1) / a.pps;
+  const long base0 = ((long)b * a.Hkv + g) * a.max_splits * G + hh;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base0 + (long)s * G) * 2]);
+  float L = 0.f, acc = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const long base = base0 + (long)s * G;
+    const float w = __builtin_amdgcn_exp2f((a.part_ml[base * 2] - M) * 1.4426950408889634f);
+    L += a.part_ml[base * 2 + 1] * w;
+    acc += a.part_o[base * kHD + d] * w;
+  }
+  out[((long)b * a.Hq + h) * kHD + d] = f32_to_bf16(acc / L);
+}
+
+// Writes the new token's k (row layout) and v (transposed layout) of every kv head at
+// position positions[b] of sequence b.
+__global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                        uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                                                        const int32_t* __restrict__ block_tables,
+                                                        const int32_t* __restrict__ positions, int Hkv, int max_pages) {
+  const int b = blockIdx.x;
+  const int pos = positions[b];
+  const long pg = block_tables[(long)b * max_pages + pos / kPage];
+  const int slot = pos % kPage;
+  for (int i = threadIdx.x; i < Hkv * kHD; i += blockDim.x) {
+    const int g = i / kHD, d = i % kHD;
+    const long head = (pg * Hkv + g) * (long)(kHD * kPage);
+    k_cache[head + slot * kHD + d] = k[(long)b * Hkv * kHD + i];
+    v_cache[head + d * kPage + slot] = v[(long)b * Hkv * kHD + i];
+  }
+}
+
+int attn_max_splits(int max_pages, int pps) { return (max_pages + pps - 1) / pps; }
+
+// pages per split: enough workgroups to fill the chip for the batch, at least 8 pages each
+int attn_pps(int B, int Hkv, int max_pages) {
+  int pps = 64;
+  while (pps > 8 && (long)B * Hkv * attn_max_splits(max_pages, pps) < 1024) pps /= 2;
+  return pps;
+}
+
+bool attn_args_ok(int B, int Hq, int Hkv, int head_dim, int page_size, int max_pages) {
+  return B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && head_dim == kHD &&
+         page_size == kPage && max_pages > 0;
+}
+
+}  // namespace
+
+extern "C" size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_pages <= 0) return 0;
+  const int pps = attn_pps(B, Hkv, max_pages);
+  const long parts = (long)B * Hq * attn_max_splits(max_pages, pps);
+  return moe_align_up((size_t)parts * kHD * sizeof(float), 256) + moe_align_up((size_t)parts * 2 * sizeof(float), 256);
+}
+
+extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,
+                                            const int32_t* block_tables, const int32_t* context_lens, int B,
+                                            int Hq, int Hkv, int head_dim, int page_size, int max_pages,
+                                            float scale, void* out, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  MOE_RETURN_IF(!attn_args_ok(B, Hq, Hkv, head_dim, page_size, max_pages), MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!q || !k_cache || !v_cache || !block_tables || !context_lens || !out, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!moe_aligned16(q) || !moe_aligned16(k_cache) || !moe_aligned16(v_cache), MOE_ERR_ALIGNMENT);
+  MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_paged_attn_workspace_bytes(B, Hq, Hkv, max_pages),
+                MOE_ERR_WORKSPACE);
+  const int pps = attn_pps(B, Hkv, max_pages);
+  const int ms = attn_max_splits(max_pages, pps);
+  WsCarver c(workspace);
+  const long parts = (long)B * Hq * ms;
+  float* part_o = c.take<float>((size_t)parts * kHD);
+  float* part_ml = c.take<float>((size_t)parts * 2);
+  AttnArgs a{(const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables, context_lens,
+             part_o, part_ml, Hq, Hkv, max_pages, ms, pps, scale};
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(paged_attn_decode_kernel, dim3(ms, Hkv, B), dim3(256), 0, s, a);
+  MOE_CHECK_LAUNCH();
+  hipLaunchKernelGGL(paged_attn_merge_kernel, dim3(Hq, B), dim3(kHD), 0, s, a, (uint16_t*)out);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+extern "C" int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
+                                    const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
+                                    int head_dim, int page_size, int max_pages, void* stream) {
+  MOE_RETURN_IF(B <= 0 || Hkv <= 0 || head_dim != kHD || page_size != kPage || max_pages <= 0, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!k || !v || !k_cache || !v_cache || !block_tables || !positions, MOE_ERR_INVALID_ARG);
+  hipLaunchKernelGGL(kv_append_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)k,
+                     (const uint16_t*)v, (uint16_t*)k_cache, (uint16_t*)v_cache, block_tables, positions, Hkv,
+                     max_pages);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}

@@ -257,3 +257,65 @@ def moe_block_fp8(hidden_states, router_weight, top_k, gate_up_proj, gate_up_pro
     if return_routing:
         return out, (logits, w, ids)
     return out
+
+
+# ---------------------------------------------------------------------------
+# paged decode attention
+# ---------------------------------------------------------------------------
+
+PAGE_SIZE = 16
+HEAD_DIM = 128
+
+
+def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """Decode attention of one new token per sequence over a paged KV cache.
+
+    The attention of ``Qwen3MoeAttention.forward`` for a decode step
+    (TF/models/qwen3_moe/modeling_qwen3_moe.py:151-191 with ``eager_attention_forward`` :96-119):
+    ``q`` bf16 [B, Hq, 128]; ``k_cache`` bf16 [pages, Hkv, 16, 128] (token rows);
+    ``v_cache`` bf16 [pages, Hkv, 128, 16] (dim rows); ``block_tables`` int32 [B, max_pages];
+    ``context_lens`` int32 [B].  Returns bf16 [B, Hq, 128].
+    """
+    _need(q, "q", torch.bfloat16, 3)
+    _need(k_cache, "k_cache", torch.bfloat16, 4)
+    _need(v_cache, "v_cache", torch.bfloat16, 4)
+    _need(block_tables, "block_tables", torch.int32, 2)
+    _need(context_lens, "context_lens", torch.int32, 1)
+    B, Hq, D = q.shape
+    P, Hkv, ps, D2 = k_cache.shape
+    if D != HEAD_DIM or D2 != HEAD_DIM or ps != PAGE_SIZE:
+        raise ValueError(f"head_dim must be {HEAD_DIM} and page size {PAGE_SIZE}")
+    if tuple(v_cache.shape) != (P, Hkv, HEAD_DIM, PAGE_SIZE):
+        raise ValueError(f"v_cache must be [pages, Hkv, {HEAD_DIM}, {PAGE_SIZE}], got {tuple(v_cache.shape)}")
+    if Hq % Hkv or Hq // Hkv > 16:
+        raise ValueError(f"Hq ({Hq}) must be a multiple of Hkv ({Hkv}) with at most 16 query heads per kv head")
+    if block_tables.shape[0] != B or context_lens.shape[0] != B:
+        raise ValueError("block_tables and context_lens need one row per sequence")
+    max_pages = block_tables.shape[1]
+    lib = _lib.load()
+    out = torch.empty_like(q)
+    ws = _ws(lib.moe_mi355x_paged_attn_workspace_bytes(B, Hq, Hkv, max_pages), q.device)
+    _lib.check(lib.moe_mi355x_paged_attn_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                                block_tables.data_ptr(), context_lens.data_ptr(), B, Hq, Hkv,
+                                                HEAD_DIM, PAGE_SIZE, max_pages, float(scale), out.data_ptr(),
+                                                ws.data_ptr(), ws.numel(), _stream(q)), "paged_attn_decode")
+    return out
+
+
+def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+              block_tables: torch.Tensor, positions: torch.Tensor) -> None:
+    """Writes one token's k, v (bf16 [B, Hkv, 128]) per sequence at ``positions`` (int32 [B])
+    into the paged cache (the cache update of modeling_qwen3_moe.py:170-171)."""
+    _need(k, "k", torch.bfloat16, 3)
+    _need(v, "v", torch.bfloat16, 3)
+    _need(k_cache, "k_cache", torch.bfloat16, 4)
+    _need(v_cache, "v_cache", torch.bfloat16, 4)
+    _need(block_tables, "block_tables", torch.int32, 2)
+    _need(positions, "positions", torch.int32, 1)
+    B, Hkv, D = k.shape
+    if tuple(v.shape) != (B, Hkv, D) or D != HEAD_DIM or k_cache.shape[1] != Hkv:
+        raise ValueError("k, v must be [B, Hkv, 128] matching the cache's kv heads")
+    _lib.check(_lib.load().moe_mi355x_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                                block_tables.data_ptr(), positions.data_ptr(), B, Hkv, HEAD_DIM,
+                                                PAGE_SIZE, block_tables.shape[1], _stream(k)), "kv_append")

@@ -1,0 +1,123 @@
+"""Paged decode attention and KV append on the GPU, through the C ABI, against the oracle
+(oracle/attn_oracle.py, pinned in tests/test_oracle_attn.py).
+
+Tolerance: the kernel applies unnormalised bf16 probabilities and divides once in fp32,
+the reference rounds the normalised probabilities to bf16 first, so outputs agree to
+bf16 rounding noise.  The bar is the layer tolerance of the MoE path: max-abs <= 2e-2 (one
+bf16 ulp of an output of magnitude 2-4 is 1.6e-2) and mean relative error <= 1e-2."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn_oracle as att
+from oracle import moe_oracle as orc
+from tests.helpers import errors, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+PAGE, D = 16, 128
+SCALE = D ** -0.5
+
+
+def build_cache(rng, lens, Hkv, q_std=1.0, n_spare=3, poison=True):
+    """Random keys / values per sequence scattered over shuffled pages; unused slots NaN."""
+    n_pages = [(L + PAGE - 1) // PAGE for L in lens]
+    total = sum(n_pages) + n_spare
+    order = rng.permutation(total)
+    kc = np.full((total, Hkv, PAGE, D), np.nan if poison else 0.0, np.float32)
+    vc = np.full((total, Hkv, D, PAGE), np.nan if poison else 0.0, np.float32)
+    max_pages = max(n_pages) + 2
+    tables = np.zeros((len(lens), max_pages), np.int32)
+    seqs = []
+    used = 0
+    for b, L in enumerate(lens):
+        pages = order[used:used + n_pages[b]]
+        used += n_pages[b]
+        tables[b, :n_pages[b]] = pages
+        k = orc.round_bf16(rng.standard_normal((L, Hkv, D)).astype(np.float32))
+        v = orc.round_bf16(rng.standard_normal((L, Hkv, D)).astype(np.float32))
+        for t in range(L):
+            kc[pages[t // PAGE], :, t % PAGE, :] = k[t]
+            vc[pages[t // PAGE], :, :, t % PAGE] = v[t]
+        seqs.append((k, v))
+    return kc, vc, tables, seqs
+
+
+def run_case(pkg, dev, lens, Hq, Hkv, seed, q_std=1.0):
+    rng = np.random.default_rng(seed)
+    kc, vc, tables, seqs = build_cache(rng, lens, Hkv)
+    q = orc.round_bf16((rng.standard_normal((len(lens), Hq, D)) * q_std).astype(np.float32))
+    out = pkg.paged_attention_decode(to_bf16(q, dev), to_bf16(kc, dev), to_bf16(vc, dev),
+                                     torch.from_numpy(tables).to(dev), torch.tensor(lens, dtype=torch.int32, device=dev),
+                                     SCALE)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = np.stack([att.decode_attention(q[b], k, v, SCALE) for b, (k, v) in enumerate(seqs)])
+    return got, ref
+
+
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([1, 2, 15, 16, 17, 33], 32, 4),          # one token, partial and exact pages
+    ([300, 511, 512, 1000], 32, 4),           # the Qwen3-30B-A3B grouping, several splits
+    ([4096, 8192], 32, 4),                    # BASELINE config 5's longest contexts
+    ([77, 130], 8, 8),                        # no grouping
+    ([200, 64], 16, 1),                       # 16 query heads on one kv head
+])
+def test_paged_attention_matches_oracle(pkg, dev, lens, Hq, Hkv):
+    got, ref = run_case(pkg, dev, lens, Hq, Hkv, seed=sum(lens))
+    max_abs, mean_rel = errors(got, ref)
+    assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
+
+
+def test_paged_attention_peaked_scores(pkg, dev):
+    # large q: softmax concentrated on few keys (exercises the running max / rescale path)
+    got, ref = run_case(pkg, dev, [700, 1500], 32, 4, seed=9, q_std=8.0)
+    max_abs, mean_rel = errors(got, ref)
+    assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
+
+
+def test_paged_attention_deterministic(pkg, dev):
+    rng = np.random.default_rng(10)
+    lens = [900, 3000, 40]
+    kc, vc, tables, _ = build_cache(rng, lens, 4, poison=False)
+    q = to_bf16(rng.standard_normal((3, 32, D)).astype(np.float32), dev)
+    args = (to_bf16(kc, dev), to_bf16(vc, dev), torch.from_numpy(tables).to(dev),
+            torch.tensor(lens, dtype=torch.int32, device=dev), SCALE)
+    a = pkg.paged_attention_decode(q, *args)
+    b = pkg.paged_attention_decode(q, *args)
+    assert torch.equal(a, b)
+
+
+def test_kv_append_places_rows(pkg, dev):
+    rng = np.random.default_rng(11)
+    B, Hkv, n_pages = 3, 4, 7
+    kc = torch.zeros((n_pages, Hkv, PAGE, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((n_pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=dev)
+    tables = np.array([[3, 1, 0], [6, 2, 0], [5, 4, 0]], np.int32)
+    pos = np.array([0, 17, 31], np.int32)
+    k = orc.round_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32))
+    v = orc.round_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32))
+    pkg.kv_append(to_bf16(k, dev), to_bf16(v, dev), kc, vc, torch.from_numpy(tables).to(dev),
+                  torch.from_numpy(pos).to(dev))
+    torch.cuda.synchronize()
+    kcn, vcn = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+    expect_k = np.zeros_like(kcn)
+    expect_v = np.zeros_like(vcn)
+    for b in range(B):
+        pg, slot = tables[b, pos[b] // PAGE], pos[b] % PAGE
+        expect_k[pg, :, slot, :] = k[b]
+        expect_v[pg, :, :, slot] = v[b]
+    assert np.array_equal(kcn, expect_k) and np.array_equal(vcn, expect_v)
+
+
+def test_paged_attention_rejects_bad_shapes(pkg, dev):
+    q = torch.zeros((2, 32, 64), dtype=torch.bfloat16, device=dev)
+    kc = torch.zeros((4, 4, PAGE, 64), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((4, 4, 64, PAGE), dtype=torch.bfloat16, device=dev)
+    t = torch.zeros((2, 2), dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        pkg.paged_attention_decode(q, kc, vc, t, t[:, 0].contiguous(), 0.1)
