@@ -10,8 +10,13 @@ the 4096-token Zipf-skewed prefill chunk (config 3) and the Qwen3-235B-A22B shap
 Weights are rotated over enough copies that one step's weights never sit in the 256 MB
 last-level cache from an earlier step; inputs rotate too, so routing changes every step.
 
+The decode-step entry (config 5) runs a 48-layer Qwen3-30B-A3B-shaped decode step at batch 128:
+per layer RMSNorm, bf16 q/k/v projections, q/k norm, rotary, KV append, paged GQA attention over
+contexts uniform in [512, 8192] (page size 16), o_proj, RMSNorm and the FP8 MoE block, all layers
+replayed as one HIP graph; it reports decode tokens/s and the per-layer MoE and attention shares.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--zipf] [--no-sweep]
-                       [--no-cpu] [--copy-probe] [--shape 30b|235b]
+                       [--no-cpu] [--no-decode-step] [--decode-step-only] [--copy-probe] [--shape 30b|235b]
   --zipf        apply the calibrated Zipf(s=1.1) router bias to the headline batch (config 3)
   --copy-probe  first run a plain 256 MiB device copy three times: the reference kernel whose
                 FETCH_SIZE / WRITE_SIZE counters calibrate the traffic measurement
@@ -294,6 +299,91 @@ def cpu_baseline(torch, layer, router, x, budget_s=20.0):
                       f"per-expert dequantise then fp32 matmul), median"}
 
 
+def decode_step_entry(pkg, torch, dev, steps=10, n_layers=48, batch=128, seed=0):
+    """a 48-layer Qwen3-30B-A3B-shaped decode step at batch 128, random-init
+    FP8 experts and bf16 dense weights, bf16 GQA paged attention (32 q / 4 kv heads, head_dim 128,
+    page 16) over context lengths uniform in [512, 8192] (the new token included).  Every
+    replay re-appends the same token, so each step does the same work."""
+    import numpy as np
+
+    from inference_server_amd import decode as dec
+
+    cfg = dec.DecoderConfig()
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 8193, size=batch).astype(np.int32)
+    pages_per_seq = (lens + dec.PAGE_SIZE - 1) // dec.PAGE_SIZE
+    n_pages = int(pages_per_seq.sum())
+    max_pages = int(pages_per_seq.max())
+    order = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed)).to(torch.int32)
+    tables = torch.zeros((batch, max_pages), dtype=torch.int32)
+    used = 0
+    for b in range(batch):
+        tables[b, : pages_per_seq[b]] = order[used: used + pages_per_seq[b]]
+        used += int(pages_per_seq[b])
+    tables = tables.to(dev)
+    ctx = torch.from_numpy(lens).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    layers = [dec.DecoderLayerWeights.random(cfg, dev, gen) for _ in range(n_layers)]
+    cache = dec.PagedKVCache(n_layers, n_pages, cfg.kv_heads, dev)
+    for t in cache.k + cache.v:
+        t.normal_(generator=gen)
+    h = torch.randn((batch, cfg.hidden), generator=gen, device=dev).to(torch.bfloat16)
+    model = dec.DecodeModel(cfg, layers, cache)
+
+    def timed(graph):
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for _ in range(steps):
+            graph.replay()
+        en.record()
+        torch.cuda.synchronize()
+        return st.elapsed_time(en) / steps
+
+    res = {}
+    with torch.no_grad():
+        for name, kw in (("full", {}), ("attention_only", {"moe": False}), ("moe_only", {"attention": False})):
+            graph, statics, out = model.capture(h, ctx - 1, ctx, tables, **kw)
+            res[name] = timed(graph)
+            assert torch.isfinite(out.float()).all(), f"non-finite hidden states ({name})"
+            del graph, statics, out
+        # the attention kernel alone, every layer's cache once (HIP events on the launch stream)
+        q = torch.randn((batch, cfg.heads, cfg.head_dim), generator=gen, device=dev).to(torch.bfloat16)
+        for i in range(2):
+            pkg.paged_attention_decode(q, cache.k[i], cache.v[i], tables, ctx, cfg.head_dim ** -0.5)
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for i in range(n_layers):
+            pkg.paged_attention_decode(q, cache.k[i], cache.v[i], tables, ctx, cfg.head_dim ** -0.5)
+        en.record()
+        torch.cuda.synchronize()
+        attn_kernel_ms = st.elapsed_time(en) / n_layers
+    kv_bytes = int(lens.sum()) * cfg.kv_heads * cfg.head_dim * 2 * 2  # K and V, bf16
+    ms = res["full"]
+    entry = {
+        "workload": f"qwen3-30b-a3b {n_layers}-layer decode step, batch {batch}, bf16 GQA paged attention "
+                    f"(32 q / 4 kv heads, head_dim 128, page 16), contexts U[512, 8192] (mean {lens.mean():.0f}), "
+                    "fp8 experts; all layers in one HIP graph",
+        "data": "synthetic (random-init weights, random KV cache)",
+        "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(batch / (ms * 1e-3), 1),
+        "us_per_layer": round(ms * 1e3 / n_layers, 2),
+        "attention_layers_us_per_layer": round(res["attention_only"] * 1e3 / n_layers, 2),
+        "moe_layers_us_per_layer": round(res["moe_only"] * 1e3 / n_layers, 2),
+        "moe_share": round(res["moe_only"] / ms, 4),
+        "attention_kernel": {"us": round(attn_kernel_ms * 1e3, 2), "kv_bytes": kv_bytes,
+                             "achieved_gbs": round(kv_bytes / (attn_kernel_ms * 1e-3) / 1e9, 1),
+                             "hbm_frac": round(kv_bytes / (attn_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+    del model, layers, cache
+    torch.cuda.empty_cache()
+    print(json.dumps({"decode_step_progress": entry}), file=sys.stderr, flush=True)
+    return entry
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,6 +394,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--zipf", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--no-decode-step", action="store_true", help="skip the 48-layer decode step (config 5)")
+    ap.add_argument("--decode-step-only", action="store_true", help="run only the 48-layer decode step")
     ap.add_argument("--shape", choices=["30b", "235b"], default="30b",
                     help="layer of the headline line: Qwen3-30B-A3B (default) or Qwen3-235B-A22B")
     args = ap.parse_args()
@@ -327,6 +419,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.decode_step_only:
+        print(json.dumps({"decode_step": decode_step_entry(pkg, torch, dev)}), flush=True)
+        return
     layer = Layer(pkg, torch, dev, S30B, n_copies=16) if args.shape == "30b" else Layer(pkg, torch, dev, S235B, n_copies=2)
     shape = layer.shape
 
@@ -375,6 +470,10 @@ def main():
             sweep.append(sweep_entry(pkg, torch, dev, big, Ts, 20 if Ts < 2048 else 10))
         del big
         line["sweep"] = sweep
+    if not args.no_decode_step and not args.no_sweep:
+        del layer.copies[1:]
+        torch.cuda.empty_cache()
+        line["decode_step"] = decode_step_entry(pkg, torch, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, layer, router, xs[0])
     print(json.dumps(line), flush=True)

@@ -1,0 +1,210 @@
+"""Decode step of a Qwen3-MoE model on the MI355X kernels.
+
+One new token per sequence per step, for a batch of sequences with a paged KV cache.  Each
+decoder layer follows ``Qwen3MoeDecoderLayer.forward``
+(TF/models/qwen3_moe/modeling_qwen3_moe.py:319-348; TF = transformers 5.15.0, the reference
+server's model code, reached through TorchBackend's batched decode, torch_backend.py:305-322):
+
+    residual = h;  x = input_layernorm(h)                              (:329-330)
+    q, k, v = q_proj(x), k_proj(x), v_proj(x);  q, k = q_norm(q), k_norm(k)   (:162-164)
+    q, k = rotary(q, k)                                               (:166-167)
+    cache.update(k, v);  a = attention(q, cache)                      (:169-186)
+    h = residual + o_proj(a)                                          (:189, :341)
+    residual = h;  h = residual + moe_block(post_attention_layernorm(h))     (:344-347)
+
+The attention (``moe_mi355x_paged_attn_decode``), the KV-cache update (``moe_mi355x_kv_append``)
+and the MoE block (``moe_mi355x_block_fp8``) are this library's HIP kernels; the dense
+projections are plain bf16 library GEMMs (hipBLASLt through torch) and the RMSNorms and the
+rotary embedding are element-wise torch ops in the reference's bf16 rounding order.
+``DecodeModel.capture`` records a whole step as one HIP graph, so a step costs one launch.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels
+
+PAGE_SIZE = kernels.PAGE_SIZE
+HEAD_DIM = kernels.HEAD_DIM
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    """Shape of a Qwen3-MoE decoder layer (configuration_qwen3_moe.py:85-109 defaults are the
+    Qwen3-30B-A3B values)."""
+
+    hidden: int = 2048
+    heads: int = 32
+    kv_heads: int = 4
+    head_dim: int = HEAD_DIM
+    experts: int = 128
+    top_k: int = 8
+    moe_intermediate: int = 768
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e6
+    norm_topk_prob: bool = True
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``Qwen3MoeRMSNorm.forward`` (modeling_qwen3_moe.py:294-299): fp32 variance and rsqrt, the
+    normalised value cast to bf16, then the bf16 weight product."""
+    xf = x.float()
+    var = xf.pow(2).mean(-1, keepdim=True)
+    return weight * (xf * torch.rsqrt(var + eps)).to(x.dtype)
+
+
+def rope_cos_sin(positions: torch.Tensor, inv_freq: torch.Tensor, dtype=torch.bfloat16):
+    """cos, sin [B, head_dim] of the default rotary embedding at ``positions``
+    (``Qwen3MoeRotaryEmbedding.forward``, modeling_qwen3_moe.py:421-436)."""
+    freqs = positions.float()[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """``x * cos + rotate_half(x) * sin`` (modeling_qwen3_moe.py:51-81); x [B, heads, d],
+    cos / sin [B, d], bf16 arithmetic."""
+    d = x.shape[-1]
+    rot = torch.cat((-x[..., d // 2:], x[..., : d // 2]), dim=-1)
+    return x * cos[:, None, :] + rot * sin[:, None, :]
+
+
+def default_inv_freq(cfg: DecoderConfig, device) -> torch.Tensor:
+    """``inv_freq`` of the default rope (modeling_rope_utils, used by modeling_qwen3_moe.py:381-436)."""
+    exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.int64, device=device).float() / cfg.head_dim
+    return 1.0 / (cfg.rope_theta ** exps)
+
+
+class PagedKVCache:
+    """Per-layer paged K / V pools in the layout of ``moe_mi355x_paged_attn_decode``:
+    K [pages, kv_heads, 16, 128] (token rows), V [pages, kv_heads, 128, 16] (dim rows)."""
+
+    def __init__(self, n_layers: int, n_pages: int, kv_heads: int, device, dtype=torch.bfloat16):
+        self.k = [torch.zeros((n_pages, kv_heads, PAGE_SIZE, HEAD_DIM), dtype=dtype, device=device)
+                  for _ in range(n_layers)]
+        self.v = [torch.zeros((n_pages, kv_heads, HEAD_DIM, PAGE_SIZE), dtype=dtype, device=device)
+                  for _ in range(n_layers)]
+        self.n_pages = n_pages
+
+
+class DecoderLayerWeights:
+    """Weights of one decoder layer.  The q/k/v projections are stored as one fused
+    [(Hq + 2 Hkv) * d, H] matrix (rows: q, then k, then v), so one GEMM serves all three."""
+
+    def __init__(self, cfg: DecoderConfig, ln1, wqkv, q_norm, k_norm, wo, ln2, router, q13, s13, q2, s2):
+        self.cfg = cfg
+        self.ln1, self.wqkv, self.q_norm, self.k_norm, self.wo, self.ln2 = ln1, wqkv, q_norm, k_norm, wo, ln2
+        self.router, self.q13, self.s13, self.q2, self.s2 = router, q13, s13, q2, s2
+
+    @classmethod
+    def random(cls, cfg: DecoderConfig, device, generator: torch.Generator, std: float = 0.02):
+        """Random-init weights of the architecture: bf16 N(0, std) matrices, unit norm weights,
+        FP8 experts block-quantised on the GPU."""
+        H, d = cfg.hidden, cfg.head_dim
+        bf = torch.bfloat16
+
+        def randn(*shape):
+            return (torch.randn(shape, generator=generator, device=device) * std).to(bf)
+
+        ones = lambda n: torch.ones(n, dtype=bf, device=device)  # noqa: E731
+        wqkv = randn((cfg.heads + 2 * cfg.kv_heads) * d, H)
+        wo = randn(H, cfg.heads * d)
+        router = randn(cfg.experts, H)
+        w13 = randn(cfg.experts, 2 * cfg.moe_intermediate, H)
+        q13, s13 = kernels.quantize_weight_fp8(w13)
+        del w13
+        w2 = randn(cfg.experts, H, cfg.moe_intermediate)
+        q2, s2 = kernels.quantize_weight_fp8(w2)
+        del w2
+        return cls(cfg, ones(H), wqkv, ones(d), ones(d), wo, ones(H), router, q13, s13, q2, s2)
+
+    @classmethod
+    def from_hf_layer(cls, layer, cfg: DecoderConfig):
+        """From a transformers ``Qwen3MoeDecoderLayer`` whose MoE block is already an
+        ``MI355XSparseMoeBlock`` (``swap_moe_blocks``)."""
+        at = layer.self_attn
+        wqkv = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0).contiguous()
+        e = layer.mlp.experts
+        return cls(cfg, layer.input_layernorm.weight.detach(), wqkv.detach(), at.q_norm.weight.detach(),
+                   at.k_norm.weight.detach(), at.o_proj.weight.detach(), layer.post_attention_layernorm.weight.detach(),
+                   layer.mlp.gate.weight.detach(), e.gate_up_proj, e.gate_up_proj_scale_inv, e.down_proj,
+                   e.down_proj_scale_inv)
+
+
+def attention_sublayer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache):
+    """``h + o_proj(attention(input_layernorm(h)))`` for one new token per sequence, appending
+    the token's k, v to the cache (modeling_qwen3_moe.py:329-341 with :151-191)."""
+    cfg = w.cfg
+    B = h.shape[0]
+    d, Hq, Hkv = cfg.head_dim, cfg.heads, cfg.kv_heads
+    x = rms_norm(h, w.ln1, cfg.rms_eps)
+    qkv = torch.nn.functional.linear(x, w.wqkv)
+    q = rms_norm(qkv[:, : Hq * d].view(B, Hq, d), w.q_norm, cfg.rms_eps)
+    k = rms_norm(qkv[:, Hq * d:(Hq + Hkv) * d].view(B, Hkv, d), w.k_norm, cfg.rms_eps)
+    v = qkv[:, (Hq + Hkv) * d:].reshape(B, Hkv, d)
+    q = apply_rotary(q, cos, sin).contiguous()
+    k = apply_rotary(k, cos, sin).contiguous()
+    kernels.kv_append(k, v.contiguous(), k_cache, v_cache, block_tables, positions)
+    a = kernels.paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens, d ** -0.5)
+    return h + torch.nn.functional.linear(a.view(B, Hq * d), w.wo)
+
+
+def moe_sublayer(w: DecoderLayerWeights, h):
+    """``h + moe_block(post_attention_layernorm(h))`` (modeling_qwen3_moe.py:344-347)."""
+    cfg = w.cfg
+    x = rms_norm(h, w.ln2, cfg.rms_eps)
+    return h + kernels.moe_block_fp8(x, w.router, cfg.top_k, w.q13, w.s13, w.q2, w.s2,
+                                     norm_topk_prob=cfg.norm_topk_prob)
+
+
+def decoder_layer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache):
+    """One full decoder layer for one decode step (modeling_qwen3_moe.py:319-348)."""
+    h = attention_sublayer(w, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache)
+    return moe_sublayer(w, h)
+
+
+class DecodeModel:
+    """The decoder-layer stack of a Qwen3-MoE model for batched decode over a paged KV cache.
+
+    ``step(h, positions, context_lens, block_tables)`` runs every layer on the hidden states of
+    the batch's new tokens ([B, hidden] bf16; ``positions`` int32 [B] = index of the new token,
+    ``context_lens`` = positions + 1, ``block_tables`` int32 [B, max_pages]).  ``capture`` records
+    one step as a HIP graph over static input buffers; ``replay`` runs it.
+    """
+
+    def __init__(self, cfg: DecoderConfig, layers: list[DecoderLayerWeights], cache: PagedKVCache):
+        self.cfg = cfg
+        self.layers = layers
+        self.cache = cache
+        dev = layers[0].wqkv.device
+        self.inv_freq = default_inv_freq(cfg, dev)
+        self._graph = None
+
+    def step(self, h, positions, context_lens, block_tables, moe: bool = True, attention: bool = True):
+        cos, sin = rope_cos_sin(positions, self.inv_freq)
+        for i, w in enumerate(self.layers):
+            if attention:
+                h = attention_sublayer(w, h, positions, context_lens, block_tables, cos, sin, self.cache.k[i],
+                                       self.cache.v[i])
+            if moe:
+                h = moe_sublayer(w, h)
+        return h
+
+    def capture(self, h, positions, context_lens, block_tables, moe: bool = True, attention: bool = True):
+        """Records one step on copies of the given inputs; returns the graph handle
+        (graph, static inputs, static output)."""
+        dev = h.device
+        statics = [t.clone() for t in (h, positions, context_lens, block_tables)]
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # warm the allocator and the library outside the capture
+            self.step(*statics, moe=moe, attention=attention)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = self.step(*statics, moe=moe, attention=attention)
+        return graph, statics, out
