@@ -157,6 +157,42 @@ int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_ca
                          int head_dim, int page_size, int max_pages, void* stream);
 
 /*
+ * RMSNorm over the last axis: out = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps)))), fp32
+ * statistics.  Replaces Qwen3MoeRMSNorm.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:294-299.
+ *   x, out bf16 [rows, cols]   weight bf16 [cols]       cols % 8 == 0, cols <= 8192
+ */
+int moe_mi355x_rms_norm(const void* x, const void* weight, int rows, int cols, float eps, void* out,
+                        void* stream);
+
+/*
+ * The per-token tail of the q/k/v projections of a decode step: per-head RMSNorm of q and k
+ * (q_norm / k_norm), the rotary embedding at positions[b] (cos / sin of positions[b] * inv_freq
+ * in fp32, cast to bf16), q written out, k and v appended to the paged cache (layout of
+ * moe_mi355x_paged_attn_decode).  Replaces Qwen3MoeAttention.forward's
+ * TF/models/qwen3_moe/modeling_qwen3_moe.py:162-171 (with apply_rotary_pos_emb :59-81 and
+ * Qwen3MoeRotaryEmbedding.forward :421-436) for one token per sequence.
+ *   qkv      bf16 [B, (Hq + 2 Hkv) * 128]  (q heads, then k heads, then v heads)
+ *   q_norm_w, k_norm_w bf16 [128]          inv_freq fp32 [64]      positions int32 [B]
+ *   q_out    bf16 [B, Hq, 128]
+ */
+int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                   const float* inv_freq, const int32_t* positions, int B, int Hq, int Hkv,
+                                   int head_dim, float eps, void* q_out, void* k_cache, void* v_cache,
+                                   const int32_t* block_tables, int page_size, int max_pages, void* stream);
+
+/*
+ * MoE sublayer of a decoder layer: out = h + moe_block(rms_norm(h, ln_weight)), with the
+ * residual add done in the top-k combine.  Replaces Qwen3MoeDecoderLayer.forward's
+ * TF/models/qwen3_moe/modeling_qwen3_moe.py:344-347 (post_attention_layernorm, the sparse
+ * block :276-281, the residual add).  Arguments as moe_mi355x_block_fp8; ids int32.
+ */
+size_t moe_mi355x_moe_sublayer_workspace_bytes(int T, int H, int I, int E, int k);
+int moe_mi355x_moe_sublayer_fp8(const void* h, const void* ln_weight, float eps, const void* w_router, int T,
+                                int H, int I, int E, int k, int renorm, const void* w13, const float* s13,
+                                const void* w2, const float* s2, void* out, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * Kernel timing (instrumentation; no counterpart in the reference).  While enabled, each
  * kernel launch of this library is bracketed by hipEvents on its stream; profile_read
  * waits for them and returns the launch count and summed duration (ms) of one slot:

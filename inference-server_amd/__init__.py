@@ -14,7 +14,7 @@ Layers:
 
 from __future__ import annotations
 
-from . import _lib, kernels  # noqa: F401
+from . import _lib, decode, kernels  # noqa: F401
 from .checkpoint import CheckpointIndex, load_moe_block, load_moe_layer  # noqa: F401
 from .experts import (  # noqa: F401
     IMPLEMENTATION_KEY,
@@ -31,7 +31,10 @@ from .kernels import (  # noqa: F401
     experts_fp8,
     kv_append,
     moe_block_fp8,
+    moe_sublayer_fp8,
     paged_attention_decode,
+    qk_norm_rope_append,
+    rms_norm,
     quantize_act_fp8,
     quantize_weight_fp8,
     route,

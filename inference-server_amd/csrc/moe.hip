@@ -27,9 +27,12 @@ namespace {
 // (moe.py:476 view(T,k,H).sum(1)); sentinel slots (ids outside [0,E)) add zero.
 // `wts` (bf16 [T, k]) non-null: the pair rows hold bf16(z) and the routing weight is applied
 // here, bf16(bf16(z) * w), the same rounding as a weighted pair row; null: already weighted.
+// `residual` (bf16 [T, H]) non-null: out = bf16(residual + bf16(sum)), the decoder layer's
+// residual add after the MoE block (TF/models/qwen3_moe/modeling_qwen3_moe.py:347).
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ pairs, const void* ids,
                                                       int id_bytes, const uint16_t* __restrict__ wts, int T,
-                                                      int k, int H, int E, uint16_t* __restrict__ out) {
+                                                      int k, int H, int E, const uint16_t* __restrict__ residual,
+                                                      uint16_t* __restrict__ out) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const int per_row = H / 8;
   if (idx >= (long)T * per_row) return;
@@ -74,6 +77,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
         acc[2 * i] += ok[u] ? lo : 0.f;
         acc[2 * i + 1] += ok[u] ? hi : 0.f;
       }
+    }
+  }
+  if (residual != nullptr) {
+    const uint4 rv = *(const uint4*)(residual + (long)t * H + c8 * 8);
+    const uint32_t ru[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = __uint_as_float(ru[i] << 16) + round_bf16(acc[2 * i]);
+      acc[2 * i + 1] = __uint_as_float(ru[i] & 0xffff0000u) + round_bf16(acc[2 * i + 1]);
     }
   }
   uint4 o;
@@ -136,7 +148,7 @@ bool experts_args_ok(int T, int H, int I, int E, int k, int id_bytes) {
 // outputs already written (the block path fuses both into its routing kernels).
 int launch_experts(const void* x, const void* ids, int id_bytes, const void* weights, int T, int H, int I,
                    int E, int k, const void* w13, const float* s13, const void* w2, const float* s2, void* out,
-                   const ExpertsWs& w, hipStream_t s, bool prepared = false) {
+                   const ExpertsWs& w, hipStream_t s, bool prepared = false, const void* residual = nullptr) {
   const int S = T * k;
   int rc;
   if (!prepared) {
@@ -153,7 +165,8 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
   const long threads = (long)T * (H / 8);
   MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      (const uint16_t*)w.pairs, ids, id_bytes,
-                     w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H, E, (uint16_t*)out);
+                     w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H, E, (const uint16_t*)residual,
+                     (uint16_t*)out);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -231,17 +244,11 @@ extern "C" size_t moe_mi355x_block_workspace_bytes(int T, int H, int I, int E, i
   return carve_block(nullptr, T, H, I, E, k).total;
 }
 
-extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,
-                                    int renorm, const void* w13, const float* s13, const void* w2,
-                                    const float* s2, void* out, void* logits, void* ids, int id_bytes,
-                                    void* weights, void* workspace, size_t workspace_bytes, void* stream) {
-  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, id_bytes), MOE_ERR_INVALID_ARG);
-  if (T == 0) return MOE_OK;
-  MOE_RETURN_IF(!x || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
-  MOE_RETURN_IF(!experts_aligned(x, w13, w2, out) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
-  const BlockWs b = carve_block(workspace, T, H, I, E, k);
-  MOE_RETURN_IF(!workspace || workspace_bytes < b.total, MOE_ERR_WORKSPACE);
-  hipStream_t s = (hipStream_t)stream;
+namespace {
+// Router + experts; `residual` non-null adds it in the combine (moe_mi355x_moe_sublayer_fp8).
+int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, int k, int renorm, const void* w13,
+               const float* s13, const void* w2, const float* s2, void* out, void* logits, void* ids, int id_bytes,
+               void* weights, const BlockWs& b, hipStream_t s, const void* residual) {
   void* lg = logits ? logits : (void*)b.logits;
   void* id_out = ids ? ids : (void*)b.ids;
   const int idb = ids ? id_bytes : 4;
@@ -258,5 +265,48 @@ extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, 
                           w.align_ws, w.align_ws_bytes, s);
     if (rc) return rc;
   }
-  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s, /*prepared=*/true);
+  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s, /*prepared=*/true, residual);
+}
+}  // namespace
+
+extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                                    int renorm, const void* w13, const float* s13, const void* w2,
+                                    const float* s2, void* out, void* logits, void* ids, int id_bytes,
+                                    void* weights, void* workspace, size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!x || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!experts_aligned(x, w13, w2, out) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
+  const BlockWs b = carve_block(workspace, T, H, I, E, k);
+  MOE_RETURN_IF(!workspace || workspace_bytes < b.total, MOE_ERR_WORKSPACE);
+  return block_impl(x, w_router, T, H, I, E, k, renorm, w13, s13, w2, s2, out, logits, ids, id_bytes, weights, b,
+                    (hipStream_t)stream, nullptr);
+}
+
+int moe_launch_rms_norm(const void* x, const void* w, int R, int C, float eps, void* out, hipStream_t s);
+
+extern "C" size_t moe_mi355x_moe_sublayer_workspace_bytes(int T, int H, int I, int E, int k) {
+  if (!experts_args_ok(T, H, I, E, k, 4)) return 0;
+  return moe_align_up((size_t)T * H * 2, 256) + carve_block(nullptr, T, H, I, E, k).total;
+}
+
+extern "C" int moe_mi355x_moe_sublayer_fp8(const void* h, const void* ln_weight, float eps, const void* w_router,
+                                           int T, int H, int I, int E, int k, int renorm, const void* w13,
+                                           const float* s13, const void* w2, const float* s2, void* out,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, 4), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!h || !ln_weight || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!experts_aligned(h, w13, w2, out) || !moe_aligned16(w_router) || !moe_aligned16(ln_weight),
+                MOE_ERR_ALIGNMENT);
+  MOE_RETURN_IF(H > 8192, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_moe_sublayer_workspace_bytes(T, H, I, E, k),
+                MOE_ERR_WORKSPACE);
+  hipStream_t s = (hipStream_t)stream;
+  void* xn = workspace;
+  const BlockWs b = carve_block((char*)workspace + moe_align_up((size_t)T * H * 2, 256), T, H, I, E, k);
+  int rc = moe_launch_rms_norm(h, ln_weight, T, H, eps, xn, s);
+  if (rc) return rc;
+  return block_impl(xn, w_router, T, H, I, E, k, renorm, w13, s13, w2, s2, out, nullptr, nullptr, 4, nullptr, b, s,
+                    h);
 }

@@ -12,10 +12,11 @@ server's model code, reached through TorchBackend's batched decode, torch_backen
     h = residual + o_proj(a)                                          (:189, :341)
     residual = h;  h = residual + moe_block(post_attention_layernorm(h))     (:344-347)
 
-The attention (``moe_mi355x_paged_attn_decode``), the KV-cache update (``moe_mi355x_kv_append``)
-and the MoE block (``moe_mi355x_block_fp8``) are this library's HIP kernels; the dense
-projections are plain bf16 library GEMMs (hipBLASLt through torch) and the RMSNorms and the
-rotary embedding are element-wise torch ops in the reference's bf16 rounding order.
+Per layer this is seven launches of this library's HIP kernels plus three library calls:
+``moe_mi355x_rms_norm`` (input_layernorm), the fused q/k/v projection GEMM (hipBLASLt through
+torch), ``moe_mi355x_qk_norm_rope_append`` (q_norm, k_norm, rotary, KV-cache update),
+``moe_mi355x_paged_attn_decode``, the o_proj GEMM and the residual add (torch), and
+``moe_mi355x_moe_sublayer_fp8`` (post_attention_layernorm, the MoE block, the residual add).
 ``DecodeModel.capture`` records a whole step as one HIP graph, so a step costs one launch.
 """
 
@@ -48,34 +49,13 @@ class DecoderConfig:
     norm_topk_prob: bool = True
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``Qwen3MoeRMSNorm.forward`` (modeling_qwen3_moe.py:294-299): fp32 variance and rsqrt, the
-    normalised value cast to bf16, then the bf16 weight product."""
-    xf = x.float()
-    var = xf.pow(2).mean(-1, keepdim=True)
-    return weight * (xf * torch.rsqrt(var + eps)).to(x.dtype)
-
-
-def rope_cos_sin(positions: torch.Tensor, inv_freq: torch.Tensor, dtype=torch.bfloat16):
-    """cos, sin [B, head_dim] of the default rotary embedding at ``positions``
-    (``Qwen3MoeRotaryEmbedding.forward``, modeling_qwen3_moe.py:421-436)."""
-    freqs = positions.float()[:, None] * inv_freq[None, :]
-    emb = torch.cat((freqs, freqs), dim=-1)
-    return emb.cos().to(dtype), emb.sin().to(dtype)
-
-
-def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """``x * cos + rotate_half(x) * sin`` (modeling_qwen3_moe.py:51-81); x [B, heads, d],
-    cos / sin [B, d], bf16 arithmetic."""
-    d = x.shape[-1]
-    rot = torch.cat((-x[..., d // 2:], x[..., : d // 2]), dim=-1)
-    return x * cos[:, None, :] + rot * sin[:, None, :]
-
-
 def default_inv_freq(cfg: DecoderConfig, device) -> torch.Tensor:
-    """``inv_freq`` of the default rope (modeling_rope_utils, used by modeling_qwen3_moe.py:381-436)."""
-    exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.int64, device=device).float() / cfg.head_dim
-    return 1.0 / (cfg.rope_theta ** exps)
+    """``inv_freq`` of the default rope, computed as ``Qwen3MoeRotaryEmbedding`` does
+    (``compute_default_rope_parameters``, modeling_qwen3_moe.py:400-418): fp32 on the CPU, then
+    moved to the device.  (The GPU's fp32 pow differs from the CPU's in the last place for a
+    third of the entries, which shifts the rotary phase at long positions.)"""
+    exps = torch.arange(0, cfg.head_dim, 2, dtype=torch.float) / cfg.head_dim
+    return (1.0 / (cfg.rope_theta ** exps)).to(device).contiguous()
 
 
 class PagedKVCache:
@@ -134,35 +114,30 @@ class DecoderLayerWeights:
                    e.down_proj_scale_inv)
 
 
-def attention_sublayer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache):
+def attention_sublayer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, inv_freq, k_cache,
+                       v_cache):
     """``h + o_proj(attention(input_layernorm(h)))`` for one new token per sequence, appending
     the token's k, v to the cache (modeling_qwen3_moe.py:329-341 with :151-191)."""
     cfg = w.cfg
     B = h.shape[0]
-    d, Hq, Hkv = cfg.head_dim, cfg.heads, cfg.kv_heads
-    x = rms_norm(h, w.ln1, cfg.rms_eps)
+    x = kernels.rms_norm(h, w.ln1, cfg.rms_eps)
     qkv = torch.nn.functional.linear(x, w.wqkv)
-    q = rms_norm(qkv[:, : Hq * d].view(B, Hq, d), w.q_norm, cfg.rms_eps)
-    k = rms_norm(qkv[:, Hq * d:(Hq + Hkv) * d].view(B, Hkv, d), w.k_norm, cfg.rms_eps)
-    v = qkv[:, (Hq + Hkv) * d:].reshape(B, Hkv, d)
-    q = apply_rotary(q, cos, sin).contiguous()
-    k = apply_rotary(k, cos, sin).contiguous()
-    kernels.kv_append(k, v.contiguous(), k_cache, v_cache, block_tables, positions)
-    a = kernels.paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens, d ** -0.5)
-    return h + torch.nn.functional.linear(a.view(B, Hq * d), w.wo)
+    q = kernels.qk_norm_rope_append(qkv, w.q_norm, w.k_norm, inv_freq, positions, cfg.heads, cfg.kv_heads,
+                                    cfg.rms_eps, k_cache, v_cache, block_tables)
+    a = kernels.paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens, cfg.head_dim ** -0.5)
+    return h + torch.nn.functional.linear(a.view(B, cfg.heads * cfg.head_dim), w.wo)
 
 
 def moe_sublayer(w: DecoderLayerWeights, h):
     """``h + moe_block(post_attention_layernorm(h))`` (modeling_qwen3_moe.py:344-347)."""
     cfg = w.cfg
-    x = rms_norm(h, w.ln2, cfg.rms_eps)
-    return h + kernels.moe_block_fp8(x, w.router, cfg.top_k, w.q13, w.s13, w.q2, w.s2,
-                                     norm_topk_prob=cfg.norm_topk_prob)
+    return kernels.moe_sublayer_fp8(h, w.ln2, cfg.rms_eps, w.router, cfg.top_k, w.q13, w.s13, w.q2, w.s2,
+                                    norm_topk_prob=cfg.norm_topk_prob)
 
 
-def decoder_layer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache):
+def decoder_layer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, inv_freq, k_cache, v_cache):
     """One full decoder layer for one decode step (modeling_qwen3_moe.py:319-348)."""
-    h = attention_sublayer(w, h, positions, context_lens, block_tables, cos, sin, k_cache, v_cache)
+    h = attention_sublayer(w, h, positions, context_lens, block_tables, inv_freq, k_cache, v_cache)
     return moe_sublayer(w, h)
 
 
@@ -184,10 +159,9 @@ class DecodeModel:
         self._graph = None
 
     def step(self, h, positions, context_lens, block_tables, moe: bool = True, attention: bool = True):
-        cos, sin = rope_cos_sin(positions, self.inv_freq)
         for i, w in enumerate(self.layers):
             if attention:
-                h = attention_sublayer(w, h, positions, context_lens, block_tables, cos, sin, self.cache.k[i],
+                h = attention_sublayer(w, h, positions, context_lens, block_tables, self.inv_freq, self.cache.k[i],
                                        self.cache.v[i])
             if moe:
                 h = moe_sublayer(w, h)

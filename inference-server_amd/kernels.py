@@ -319,3 +319,72 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     _lib.check(_lib.load().moe_mi355x_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                                 block_tables.data_ptr(), positions.data_ptr(), B, Hkv, HEAD_DIM,
                                                 PAGE_SIZE, block_tables.shape[1], _stream(k)), "kv_append")
+
+
+# ---------------------------------------------------------------------------
+# decoder-layer pieces around the attention and the MoE block
+# ---------------------------------------------------------------------------
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``Qwen3MoeRMSNorm.forward`` (TF/models/qwen3_moe/modeling_qwen3_moe.py:294-299) over the
+    last axis of a bf16 tensor."""
+    _need(x, "x", torch.bfloat16)
+    _need(weight, "weight", torch.bfloat16, 1)
+    C = x.shape[-1]
+    if weight.shape[0] != C:
+        raise ValueError(f"weight has {weight.shape[0]} entries for {C} columns")
+    out = torch.empty_like(x)
+    _lib.check(_lib.load().moe_mi355x_rms_norm(x.data_ptr(), weight.data_ptr(), x.numel() // max(C, 1), C,
+                                               float(eps), out.data_ptr(), _stream(x)), "rms_norm")
+    return out
+
+
+def qk_norm_rope_append(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+                        inv_freq: torch.Tensor, positions: torch.Tensor, num_heads: int, num_kv_heads: int,
+                        eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        block_tables: torch.Tensor) -> torch.Tensor:
+    """q/k RMSNorm, rotary embedding and the KV-cache append of one new token per sequence
+    (modeling_qwen3_moe.py:162-171).  ``qkv`` bf16 [B, (Hq + 2 Hkv) * 128]; returns q bf16
+    [B, Hq, 128]; k and v go into the paged cache at ``positions``."""
+    _need(qkv, "qkv", torch.bfloat16, 2)
+    _need(q_norm_weight, "q_norm_weight", torch.bfloat16, 1)
+    _need(k_norm_weight, "k_norm_weight", torch.bfloat16, 1)
+    _need(inv_freq, "inv_freq", torch.float32, 1)
+    _need(positions, "positions", torch.int32, 1)
+    _need(k_cache, "k_cache", torch.bfloat16, 4)
+    _need(v_cache, "v_cache", torch.bfloat16, 4)
+    _need(block_tables, "block_tables", torch.int32, 2)
+    B = qkv.shape[0]
+    if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * HEAD_DIM or inv_freq.shape[0] != HEAD_DIM // 2:
+        raise ValueError("qkv must be [B, (Hq + 2 Hkv) * 128] and inv_freq [64]")
+    if k_cache.shape[1] != num_kv_heads or positions.shape[0] != B or block_tables.shape[0] != B:
+        raise ValueError("cache kv heads, positions and block tables must match the batch")
+    q = torch.empty((B, num_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
+    _lib.check(_lib.load().moe_mi355x_qk_norm_rope_append(
+        qkv.data_ptr(), q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), inv_freq.data_ptr(), positions.data_ptr(),
+        B, num_heads, num_kv_heads, HEAD_DIM, float(eps), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), PAGE_SIZE, block_tables.shape[1], _stream(qkv)), "qk_norm_rope_append")
+    return q
+
+
+def moe_sublayer_fp8(hidden_states, ln_weight, eps, router_weight, top_k, gate_up_proj, gate_up_proj_scale_inv,
+                     down_proj, down_proj_scale_inv, norm_topk_prob: bool = True) -> torch.Tensor:
+    """``h + moe_block(post_attention_layernorm(h))`` (modeling_qwen3_moe.py:344-347): the RMSNorm,
+    the MoE block and the residual add in one entry point."""
+    _need(hidden_states, "hidden_states", torch.bfloat16, 2)
+    _need(ln_weight, "ln_weight", torch.bfloat16, 1)
+    _need(router_weight, "router_weight", torch.bfloat16, 2)
+    E, H, I = _check_expert_weights(gate_up_proj, gate_up_proj_scale_inv, down_proj, down_proj_scale_inv)
+    T = hidden_states.shape[0]
+    if hidden_states.shape[1] != H or tuple(router_weight.shape) != (E, H) or ln_weight.shape[0] != H:
+        raise ValueError("hidden_states, ln_weight and router_weight must match the experts' hidden size")
+    lib = _lib.load()
+    out = torch.empty_like(hidden_states)
+    ws = _ws(lib.moe_mi355x_moe_sublayer_workspace_bytes(T, H, I, E, top_k), hidden_states.device)
+    _lib.check(lib.moe_mi355x_moe_sublayer_fp8(
+        hidden_states.data_ptr(), ln_weight.data_ptr(), float(eps), router_weight.data_ptr(), T, H, I, E, top_k,
+        int(norm_topk_prob), gate_up_proj.data_ptr(), gate_up_proj_scale_inv.data_ptr(), down_proj.data_ptr(),
+        down_proj_scale_inv.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(hidden_states)),
+        "moe_sublayer_fp8")
+    return out

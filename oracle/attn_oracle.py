@@ -21,8 +21,9 @@ Parity status (how each is pinned is in ``tests/test_oracle.py``):
 * ``decode_attention``: pinned (pure-Python brute force on tiny shapes, closed forms:
   identical keys give the mean of V, a dominant key selects its V row, kv-head mapping;
   golden vectors written by transformers' ``eager_attention_forward`` on CPU).
-* ``rms_norm``, ``rotary``: pinned (golden vectors of transformers' ``Qwen3MoeRMSNorm`` and
-  ``apply_rotary_pos_emb`` on CPU; closed forms: rotation preserves pair norms, position 0
+* ``rms_norm``, ``rotary``, ``rope_cos_sin``, ``default_inv_freq``: pinned (golden vectors of
+  transformers' ``Qwen3MoeRMSNorm``, ``Qwen3MoeRotaryEmbedding`` (its inv_freq and cos / sin)
+  and ``apply_rotary_pos_emb`` on CPU; closed forms: rotation preserves pair norms, position 0
   is the identity).
 * ``gather_paged``: pinned (round trip against ``scatter_paged`` on a shuffled page table).
 """
@@ -45,14 +46,25 @@ def rms_norm(x, weight, eps: float = 1e-6) -> np.ndarray:
     return round_bf16(np.asarray(weight, np.float32) * y)
 
 
-def rope_cos_sin(positions, head_dim: int = 128, theta: float = 1e6):
-    """cos, sin [len(positions), head_dim] of the default rope (modeling_qwen3_moe.py:381-436):
-    ``freqs = pos * inv_freq`` in fp32, ``emb = cat(freqs, freqs)``, cast to bf16."""
-    inv_freq = (1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.int64).astype(np.float32) / head_dim))).astype(
+def default_inv_freq(head_dim: int = 128, theta: float = 1e6) -> np.ndarray:
+    """``1 / theta ** (2i / d)`` in fp32 (``compute_default_rope_parameters``,
+    modeling_qwen3_moe.py:400-418).  The reference evaluates the pow with torch's CPU fp32 pow;
+    numpy's fp32 pow differs from it in the last place for some entries, so tests that need the
+    reference's exact phases pass its own inv_freq (stored with the golden vectors)."""
+    return (1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.int64).astype(np.float32) / head_dim))).astype(
         np.float32)
+
+
+def rope_cos_sin(positions, head_dim: int = 128, theta: float = 1e6, inv_freq=None):
+    """cos, sin [len(positions), head_dim] of the default rope (modeling_qwen3_moe.py:381-436):
+    ``freqs = pos * inv_freq`` in fp32, ``emb = cat(freqs, freqs)``, cast to bf16; cos / sin
+    evaluated in float64 and rounded (within one fp32 ulp of any accurate fp32 cos / sin)."""
+    if inv_freq is None:
+        inv_freq = default_inv_freq(head_dim, theta)
+    inv_freq = np.asarray(inv_freq, np.float32)
     freqs = np.asarray(positions, np.float32)[:, None] * inv_freq[None, :]
-    emb = np.concatenate([freqs, freqs], axis=-1)
-    return round_bf16(np.cos(emb)), round_bf16(np.sin(emb))
+    emb = np.concatenate([freqs, freqs], axis=-1).astype(np.float64)
+    return round_bf16(np.cos(emb).astype(np.float32)), round_bf16(np.sin(emb).astype(np.float32))
 
 
 def rotary(x, cos, sin) -> np.ndarray:

@@ -90,6 +90,7 @@ def run_case(name, Hq, Hkv, L, H, seed):
         path,
         shape=np.array([Hq, Hkv, L, H, seed], dtype=np.int64),
         digests=np.array([digest(a) for a in (q, k, v, x, w)]),
+        inv_freq=rope.inv_freq.numpy().astype(np.float32),
         rmsnorm_bf16=bits(x_norm),
         cos_bf16=bits(cos[0]),
         sin_bf16=bits(sin[0]),

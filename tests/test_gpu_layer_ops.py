@@ -1,0 +1,91 @@
+"""Fused decoder-layer pieces on the GPU, through the C ABI, against the oracle
+(oracle/attn_oracle.py: RMSNorm and rotary pinned by transformers golden vectors).
+
+* RMSNorm: within 1 bf16 ulp of the oracle, >= 99% bit-identical (the fp32 sum of squares
+  is accumulated in another order).
+* q/k norm + rotary + KV append: q and k within 1 bf16 ulp of the oracle's norm-then-rotary
+  chain given the same inv_freq, >= 98% bit-identical (the fp32 sum of squares is accumulated
+  in another order; the device's fp32 cos / sin are within one ulp of the float64-rounded
+  ones); v placed bit-exactly.
+* MoE sublayer: bit-identical to RMSNorm, the MoE block and a bf16 residual add run as
+  separate calls.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn_oracle as att
+from oracle import moe_oracle as orc
+from tests.helpers import gpu_weights, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+D, PAGE = 128, 16
+
+
+def ulps(a, b):
+    def ordered(x):
+        bits = orc.bf16_bits(x).astype(np.int32)
+        return np.where(bits & 0x8000, -(bits & 0x7FFF), bits)
+    return np.abs(ordered(a) - ordered(b))
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (300, 128), (5, 4096), (1, 8)])
+def test_rms_norm(pkg, dev, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x = orc.round_bf16((rng.standard_normal((rows, cols)) * 3).astype(np.float32))
+    w = orc.round_bf16((1 + 0.1 * rng.standard_normal(cols)).astype(np.float32))
+    out = pkg.rms_norm(to_bf16(x, dev), to_bf16(w, dev), 1e-6).float().cpu().numpy()
+    d = ulps(out, att.rms_norm(x, w, 1e-6))
+    assert d.max() <= 1 and (d == 0).mean() >= 0.99
+
+
+@pytest.mark.parametrize("Hq,Hkv,B", [(32, 4, 7), (4, 2, 3)])
+def test_qk_norm_rope_append(pkg, dev, Hq, Hkv, B):
+    from inference_server_amd import decode as dec
+
+    rng = np.random.default_rng(B)
+    nh = Hq + 2 * Hkv
+    qkv = orc.round_bf16(rng.standard_normal((B, nh * D)).astype(np.float32))
+    qw = orc.round_bf16((1 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    kw = orc.round_bf16((1 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    pos = rng.integers(0, 8000, size=B).astype(np.int32)
+    max_pages = 8000 // PAGE + 1
+    n_pages = B * max_pages
+    tables = rng.permutation(n_pages).astype(np.int32).reshape(B, max_pages)
+    kc = torch.zeros((n_pages, Hkv, PAGE, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((n_pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=dev)
+    inv_freq = dec.default_inv_freq(dec.DecoderConfig(), dev)
+    q = pkg.qk_norm_rope_append(to_bf16(qkv, dev), to_bf16(qw, dev), to_bf16(kw, dev), inv_freq,
+                                torch.from_numpy(pos).to(dev), Hq, Hkv, 1e-6, kc, vc, torch.from_numpy(tables).to(dev))
+    torch.cuda.synchronize()
+    cos, sin = att.rope_cos_sin(pos, D, 1e6, inv_freq=inv_freq.cpu().numpy())
+    heads = qkv.reshape(B, nh, D)
+    q_ref = att.rotary(att.rms_norm(heads[:, :Hq], qw, 1e-6), cos, sin)
+    k_ref = att.rotary(att.rms_norm(heads[:, Hq:Hq + Hkv], kw, 1e-6), cos, sin)
+    d = ulps(q.float().cpu().numpy(), q_ref)
+    assert d.max() <= 1 and (d == 0).mean() >= 0.98, (d.max(), (d == 0).mean())
+    kcn, vcn = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+    for b in range(B):
+        pg, slot = tables[b, pos[b] // PAGE], pos[b] % PAGE
+        dk = ulps(kcn[pg, :, slot, :], k_ref[b])
+        assert dk.max() <= 1 and (dk == 0).mean() >= 0.95
+        assert np.array_equal(vcn[pg, :, :, slot], heads[b, Hq + Hkv:])
+
+
+@pytest.mark.parametrize("T", [1, 64, 600])
+def test_moe_sublayer_equals_separate_calls(pkg, dev, T):
+    E, H, I, k = 32, 512, 256, 4
+    q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=T)
+    g = torch.Generator(device=dev).manual_seed(T)
+    h = (torch.randn((T, H), generator=g, device=dev) * 2).to(torch.bfloat16)
+    ln = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    fused = pkg.moe_sublayer_fp8(h, ln, 1e-6, wr, k, q13, s13, q2, s2)
+    x = pkg.rms_norm(h, ln, 1e-6)
+    sep = h + pkg.moe_block_fp8(x, wr, k, q13, s13, q2, s2)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, sep)

@@ -42,7 +42,10 @@ def test_golden_decoder_pieces(case):
 
     # rotary cos / sin and their application to q (position L-1) and every k
     L = cfg["L"]
-    cos, sin = att.rope_cos_sin(np.arange(L), mga.HEAD_DIM, mga.THETA)
+    inv = g["inv_freq"]
+    # numpy and torch evaluate the fp32 pow and divide with different libm code: <= 2 ulps apart
+    assert np.abs(att.default_inv_freq(mga.HEAD_DIM, mga.THETA).view(np.int32) - inv.view(np.int32)).max() <= 2
+    cos, sin = att.rope_cos_sin(np.arange(L), mga.HEAD_DIM, mga.THETA, inv_freq=inv)
     assert ulps(cos, gold["cos_bf16"]).max() <= 1 and ulps(sin, gold["sin_bf16"]).max() <= 1
     # with the reference's own cos / sin the application is bit-exact
     q_rot = att.rotary(q[None], gold["cos_bf16"][L - 1:], gold["sin_bf16"][L - 1:])[0]
@@ -149,3 +152,16 @@ def test_rope_position_zero_is_identity_and_preserves_norms():
     n0 = np.hypot(x[1, :, :64], x[1, :, 64:])
     n1 = np.hypot(y[1, :, :64], y[1, :, 64:])
     assert np.allclose(n0, n1, rtol=2e-2, atol=1e-2)
+
+
+def test_product_inv_freq_is_the_references():
+    """The decode path's inv_freq (computed like transformers' rotary embedding) equals the
+    reference's golden inv_freq bit for bit."""
+    import torch
+
+    import __graft_entry__
+
+    dec = __graft_entry__.load_package().decode
+    g = np.load(os.path.join(GOLDEN, "attn_g8_l300.npz"))
+    got = dec.default_inv_freq(dec.DecoderConfig(), torch.device("cpu")).numpy()
+    assert np.array_equal(got, g["inv_freq"])
