@@ -45,7 +45,9 @@ struct AttnArgs {
   float scale;
 };
 
-__global__ __launch_bounds__(256) void paged_attn_decode_kernel(AttnArgs a) {
+// four waves per SIMD (at most 128 registers): each wave has one page in flight, so occupancy
+// is what keeps the HBM busy
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void paged_attn_decode_kernel(AttnArgs a) {
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int G = a.Hq / a.Hkv;
   const int ctx = a.context_lens[b];
@@ -78,35 +80,43 @@ __global__ __launch_bounds__(256) void paged_attn_decode_kernel(AttnArgs a) {
   for (int n = 0; n < 8; ++n) o[n] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   // operands of one page: K rows (lane: key lr, dims 32 kk + 8 lg) and V^T (lane: keys
-  // 4 lg .. +4 of dim 16 n + lr)
+  // 4 lg .. +4 of dim 16 n + lr).  One register set each: the next page's K is loaded as soon
+  // as the score MFMAs have read this page's, its V after the output MFMAs, so both stay in
+  // flight through most of an iteration without a second buffer (occupancy over depth).
   uint4 kr[4];
   uint2 vr[8];
-  auto load_page = [&](int p) __attribute__((always_inline)) {
-    const long pg = btab[p];
+  // page ids of this wave's pages p_begin + wave + 4 i, one per lane, fetched up front so that
+  // the K / V loads of a page do not wait on a dependent block-table load
+  const int my_page = (p_begin + wave + kAttnWaves * lane < p_end) ? btab[p_begin + wave + kAttnWaves * lane] : 0;
+  auto page_of = [&](int p) __attribute__((always_inline)) {
+    return (long)__builtin_amdgcn_readlane(my_page, (p - p_begin - wave) / kAttnWaves);
+  };
+  auto load_k = [&](int p) __attribute__((always_inline)) {
+    const long pg = page_of(p);
     const uint16_t* kb = a.k_cache + (pg * a.Hkv + g) * kv_head_stride;
-    const uint16_t* vb = a.v_cache + (pg * a.Hkv + g) * kv_head_stride;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) kr[kk] = *(const uint4*)(kb + lr * kHD + 32 * kk + 8 * lg);
+  };
+  auto load_v = [&](int p) __attribute__((always_inline)) {
+    const long pg = page_of(p);
+    const uint16_t* vb = a.v_cache + (pg * a.Hkv + g) * kv_head_stride;
 #pragma unroll
     for (int n = 0; n < 8; ++n) vr[n] = *(const uint2*)(vb + (16 * n + lr) * kPage + 4 * lg);
   };
 
   int p = p_begin + wave;
-  if (p < p_end) load_page(p);
+  if (p < p_end) {
+    load_k(p);
+    load_v(p);
+  }
   for (; p < p_end; p += kAttnWaves) {
-    uint4 kc[4];
-    uint2 vc[8];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) kc[kk] = kr[kk];
-#pragma unroll
-    for (int n = 0; n < 8; ++n) vc[n] = vr[n];
-    if (p + kAttnWaves < p_end) load_page(p + kAttnWaves);  // next page of this wave in flight
-
+    const bool more = p + kAttnWaves < p_end;
     // scores S^T: lane holds keys 4 lg + i of head lr
     v4f s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kc[kk]), qop[kk], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kr[kk]), qop[kk], s, 0, 0, 0);
+    if (more) load_k(p + kAttnWaves);
     const int key0 = p * kPage + 4 * lg;
     float sv[4];
 #pragma unroll
@@ -143,7 +153,7 @@ __global__ __launch_bounds__(256) void paged_attn_decode_kernel(AttnArgs a) {
     const int live_keys = ctx - key0;  // keys 4 lg + j with j < live_keys are valid
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      uint2 v = vc[n];
+      uint2 v = vr[n];
       if (live_keys < 4) {
         if (live_keys <= 0) v.x = v.y = 0u;
         else if (live_keys == 1) { v.x &= 0xffffu; v.y = 0u; }
@@ -159,6 +169,7 @@ __global__ __launch_bounds__(256) void paged_attn_decode_kernel(AttnArgs a) {
       vb[3] = (short)(v.y >> 16);
       o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[n], 0, 0, 0);
     }
+    if (more) load_v(p + kAttnWaves);
   }
 
   // merge the 4 waves: per head max, sum and O rows (heads 4 lg + i, dims 16 n + lr)
@@ -243,7 +254,7 @@ int attn_max_splits(int max_pages, int pps) { return (max_pages + pps - 1) / pps
 
 // pages per split: enough workgroups to fill the chip for the batch, at least 8 pages each
 int attn_pps(int B, int Hkv, int max_pages) {
-  int pps = 64;
+  int pps = 64;  // <= 4 waves x 64 lanes: a wave's page ids fit one register
   while (pps > 8 && (long)B * Hkv * attn_max_splits(max_pages, pps) < 1024) pps /= 2;
   return pps;
 }
