@@ -88,6 +88,40 @@ __global__ __launch_bounds__(kChunk) void align_scan_kernel(int32_t* bc, int nb,
   }
 }
 
+// Large S, passes 2 + 3 in one launch: every workgroup reduces all chunk histograms (its
+// chunk's starting slot per expert = offset of the expert + counts of the earlier chunks),
+// workgroup 0 writes counts, offsets and the tile list, and each places its chunk stably.
+__global__ __launch_bounds__(kChunk) void align_scan_scatter_kernel(const void* ids, int id_bytes, int S, int E,
+                                                                    int block_m, const int32_t* __restrict__ bc,
+                                                                    int nb, int32_t* perm, int32_t* counts,
+                                                                    int32_t* offsets, int32_t* tiles,
+                                                                    int32_t* n_tiles) {
+  __shared__ int s_cnt[kBuckets];
+  __shared__ int s_off[kBuckets];
+  __shared__ int s_toff[kBuckets];
+  __shared__ int s_base[kBuckets];
+  __shared__ int s_wcnt[kWaves][kBuckets];
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    int tot = 0, pre = 0;
+#pragma unroll 8
+    for (int c = 0; c < nb; ++c) {
+      const int v = bc[(long)c * (E + 1) + e];
+      tot += v;
+      pre += c < b ? v : 0;
+    }
+    s_cnt[e] = tot;
+    s_base[e] = pre;
+  }
+  __syncthreads();
+  scan_counts(s_cnt, E, block_m, s_off, s_toff);
+  __syncthreads();
+  if (b == 0) emit_meta(s_cnt, s_off, s_toff, E, block_m, counts, offsets, tiles, n_tiles);
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_base[e] += s_off[e];
+  __syncthreads();
+  scatter_chunk(ids, id_bytes, S, E, b * kChunk, s_base, s_wcnt, perm);
+}
+
 // Large S, pass 3: stable placement of chunk b starting from its per-expert slots.
 __global__ __launch_bounds__(kChunk) void align_scatter_kernel(const void* ids, int id_bytes, int S, int E,
                                                                const int32_t* bases, int32_t* perm) {
@@ -111,6 +145,10 @@ extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E) {
   return moe_align_up(nb * (E + 1) * sizeof(int32_t), 256);
 }
 
+int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
+                             int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                             hipStream_t s);
+
 int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
                      int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles, void* workspace,
                      size_t workspace_bytes, hipStream_t s) {
@@ -125,11 +163,17 @@ int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, i
   int32_t* bc = (int32_t*)workspace;
   MOE_LAUNCH(MOE_PROF_ALIGN, s, align_count_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E, bc);
   MOE_CHECK_LAUNCH();
-  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scan_kernel, dim3(1), dim3(kChunk), 0, s, bc, nb, E, block_m, counts, offsets,
-                     tiles, n_tiles);
-  MOE_CHECK_LAUNCH();
-  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
-                     (const int32_t*)bc, perm);
+  return moe_launch_align_counted(ids, id_bytes, S, E, block_m, bc, perm, counts, offsets, tiles, n_tiles, s);
+}
+
+// The rest of the large-S align once the chunk histograms bc [nb, E + 1] are filled (by
+// align_count_kernel, or by the top-k kernel of the block path).
+int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
+                             int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                             hipStream_t s) {
+  const int nb = (S + kChunk - 1) / kChunk;
+  MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scan_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
+             block_m, bc, nb, perm, counts, offsets, tiles, n_tiles);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }

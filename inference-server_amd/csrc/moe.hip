@@ -15,7 +15,11 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
-                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles);
+                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                     int32_t* chunk_counts);
+int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
+                             int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                             hipStream_t s);
 extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E);
 bool moe_route_can_fuse_align(int T, int E, int k);
 extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m);
@@ -254,13 +258,20 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
   const int idb = ids ? id_bytes : 4;
   void* wt = weights ? weights : (void*)b.weights;
   const ExpertsWs w = carve_experts(b.experts_ws, T, H, I, E, k);
-  // decode batches: x quantisation rides in the router GEMM, align in the top-k kernel
+  // decode batches: x quantisation rides in the router GEMM, align in the top-k kernel; large
+  // batches: the top-k kernel fills the expert sort's chunk histograms (cleared by the router
+  // GEMM), and one launch finishes the sort
   const bool fused = moe_route_can_fuse_align(T, E, k);
+  const bool counted = !fused && w.align_ws_bytes > 0;
   int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s,
                             w.xq, w.sx, w.block_m, fused ? w.perm : nullptr, w.counts, w.offsets, w.tiles,
-                            w.n_tiles);
+                            w.n_tiles, counted ? (int32_t*)w.align_ws : nullptr);
   if (rc) return rc;
-  if (!fused) {
+  if (counted) {
+    rc = moe_launch_align_counted(id_out, idb, T * k, E, w.block_m, (const int32_t*)w.align_ws, w.perm, w.counts,
+                                  w.offsets, w.tiles, w.n_tiles, s);
+    if (rc) return rc;
+  } else if (!fused) {
     rc = moe_launch_align(id_out, idb, T * k, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
                           w.align_ws, w.align_ws_bytes, s);
     if (rc) return rc;

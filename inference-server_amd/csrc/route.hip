@@ -23,7 +23,11 @@ constexpr int kMaxKSplit = 16;      // router K-split partials summed by the top
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wr, int T, int H,
                                                           int E, int kchunk, float* __restrict__ part,
-                                                          uint8_t* __restrict__ xq, float* __restrict__ sx) {
+                                                          uint8_t* __restrict__ xq, float* __restrict__ sx,
+                                                          int32_t* __restrict__ zero, int nzero) {
+  // workgroup 0 clears the expert sort's chunk histograms that the top-k kernel fills next
+  if (zero != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+    for (int i = threadIdx.x; i < nzero; i += blockDim.x) zero[i] = 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t0 = blockIdx.x * kRouterTileT;
   const int kbeg = blockIdx.z * kchunk;
@@ -110,7 +114,10 @@ constexpr int kRtT = 64, kRtE = 128;
 __global__ __launch_bounds__(256) void router_gemm_tiled_kernel(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ wr, int T, int H,
                                                                 int E, int kchunk, float* __restrict__ part,
-                                                                uint8_t* __restrict__ xq, float* __restrict__ sx) {
+                                                                uint8_t* __restrict__ xq, float* __restrict__ sx,
+                                                                int32_t* __restrict__ zero, int nzero) {
+  if (zero != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+    for (int i = threadIdx.x; i < nzero; i += blockDim.x) zero[i] = 0;
   __shared__ uint4 s_x[kRtT * 16];
   __shared__ uint4 s_w[kRtE * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -306,18 +313,25 @@ __device__ __forceinline__ void store_route(void* ids, int id_bytes, uint16_t* w
     ((int32_t*)ids)[idx] = e;
 }
 
-// One wave per token, 4 tokens per workgroup.
+// One wave per token, 4 tokens per workgroup.  With `bc` (zeroed beforehand) each routed pair
+// also counts into its 1024-pair chunk's expert histogram bc[chunk][e], the first pass of the
+// expert sort (integer atomics: the counts do not depend on their order).
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ part, int ksplit,
                                                            const uint16_t* __restrict__ logits_in, int T,
                                                            int E, int k, int renorm,
                                                            uint16_t* __restrict__ logits_out, void* ids,
-                                                           int id_bytes, uint16_t* __restrict__ weights) {
+                                                           int id_bytes, uint16_t* __restrict__ weights,
+                                                           int32_t* __restrict__ bc) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   int my_e;
   float my_w;
   route_token(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
+  if (bc != nullptr && lane < k) {
+    const int pair = t * k + lane;
+    atomicAdd(&bc[(long)(pair / kChunk) * (E + 1) + my_e], 1);
+  }
   if (lane < k) store_route(ids, id_bytes, weights, (long)t * k + lane, my_e, my_w);
 }
 
@@ -426,9 +440,12 @@ bool moe_route_can_fuse_align(int T, int E, int k) {
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
-                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles) {
+                     int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                     int32_t* chunk_counts) {
   if (T == 0) return MOE_OK;
   const bool quant = xq != nullptr;
+  MOE_RETURN_IF(chunk_counts != nullptr && perm != nullptr, MOE_ERR_INVALID_ARG);
+  const int nzero = chunk_counts ? (int)(((long)T * k + kChunk - 1) / kChunk) * (E + 1) : 0;
   MOE_RETURN_IF(quant && H % MOE_GROUP, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(perm != nullptr && !moe_route_can_fuse_align(T, E, k), MOE_ERR_INVALID_ARG);
   const int ks = route_ksplit(T, H, E);
@@ -440,11 +457,11 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   if (tiled) {
     dim3 g1((T + kRtT - 1) / kRtT, (E + kRtE - 1) / kRtE, ks_eff);
     MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_tiled_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
-               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx);
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
   } else {
     dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
     MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
-               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx);
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
   }
   MOE_CHECK_LAUNCH();
   if (perm != nullptr) {
@@ -453,7 +470,8 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
                n_tiles);
   } else {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
-               (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights);
+               (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights,
+               chunk_counts);
   }
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -468,7 +486,7 @@ extern "C" int moe_mi355x_route(const void* x, const void* w_router, int T, int 
   MOE_RETURN_IF(!moe_aligned16(x) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
   return moe_launch_route(x, w_router, T, H, E, k, renorm, logits, ids, id_bytes, weights, workspace,
                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, 0, nullptr, nullptr, nullptr,
-                          nullptr, nullptr);
+                          nullptr, nullptr, nullptr);
 }
 
 extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, int renorm, void* ids,
@@ -478,7 +496,7 @@ extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, 
   MOE_RETURN_IF(!logits || !ids || !weights, MOE_ERR_INVALID_ARG);
   MOE_LAUNCH(MOE_PROF_TOPK, (hipStream_t)stream, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0,
              (hipStream_t)stream, (const float*)nullptr, 0, (const uint16_t*)logits, T, E, k, renorm,
-             (uint16_t*)nullptr, ids, id_bytes, (uint16_t*)weights);
+             (uint16_t*)nullptr, ids, id_bytes, (uint16_t*)weights, (int32_t*)nullptr);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
