@@ -237,8 +237,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   int rc;
   if (block_m == 16)
     rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
-  else if (block_m == 32)
-    rc = launch_gemm<MODE_GATE_UP, 2, 4>(g1, max_tiles, s);
+  else if (block_m == 32)  // no K split: 64 h columns per workgroup share one load of the tile's rows
+    rc = launch_gemm<MODE_GATE_UP, 2, 1>(g1, max_tiles, s);
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
@@ -250,7 +250,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
     rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
   else if (block_m == 32)
-    rc = launch_gemm<MODE_DOWN, 2, 2, 2>(g2, max_tiles, s);
+    rc = launch_gemm<MODE_DOWN, 2, 1, 2>(g2, max_tiles, s);
   else
     rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
   return rc;
