@@ -137,7 +137,8 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
  *   k_cache      bf16 [pages, Hkv, 16, 128] (token rows)
  *   v_cache      bf16 [pages, Hkv, 128, 16] (transposed: dim rows)
  *   block_tables int32 [B, max_pages]       page of each 16-token block of a sequence
- *   context_lens int32 [B]                  >= 1, <= 16 * max_pages
+ *   context_lens int32 [B]                  >= 1, <= 16 * max_pages (device data: a larger value
+ *                                           is clamped to the table, 0 gives a zero output)
  * The KV layout is this library's; the reference keeps a contiguous per-layer cache.
  * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16.
  */
@@ -151,6 +152,8 @@ int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void*
  * KV-cache append of one token per sequence at position positions[b] (the cache update of
  * Qwen3MoeAttention.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:170-171, in the paged
  * layout above).  k, v: bf16 [B, Hkv, 128] (k after k_norm and rotary embedding).
+ * positions[b] in [0, 16 * max_pages), its page allocated in block_tables; a position outside
+ * the table writes nothing.
  */
 int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
                          const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
@@ -174,6 +177,8 @@ int moe_mi355x_rms_norm(const void* x, const void* weight, int rows, int cols, f
  *   qkv      bf16 [B, (Hq + 2 Hkv) * 128]  (q heads, then k heads, then v heads)
  *   q_norm_w, k_norm_w bf16 [128]          inv_freq fp32 [64]      positions int32 [B]
  *   q_out    bf16 [B, Hq, 128]
+ * positions[b] in [0, 16 * max_pages), its page allocated in block_tables; for a position
+ * outside the table q is written and the cache is not.
  */
 int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                                    const float* inv_freq, const int32_t* positions, int B, int Hq, int Hkv,

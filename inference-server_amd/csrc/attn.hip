@@ -37,6 +37,12 @@ constexpr int kAttnWaves = 4;
 
 __device__ __forceinline__ float bf16_round(float f) { return (float)(__bf16)f; }
 
+// Pages of a context, clamped to the block table's width (context lengths are device data:
+// a value past the table would read beyond it).  Negative lengths count as empty.
+__device__ __forceinline__ int attn_pages(int ctx, int max_pages) {
+  return ctx <= 0 ? 0 : min((ctx + kPage - 1) / kPage, max_pages);
+}
+
 struct AttnArgs {
   const uint16_t* q;           // [B, Hq, 128] bf16
   const uint16_t* k_cache;     // [pages, Hkv, 16, 128] bf16
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       const int bb = b0 + (int)threadIdx.x;
       int n_it = 0;
       if (bb < a.B) {
-        const int np = (a.context_lens[bb] + kPage - 1) / kPage;
+        const int np = attn_pages(a.context_lens[bb], a.max_pages);
         n_it = (np + a.pps - 1) / a.pps * a.Hkv;
       }
       int incl = n_it;
@@ -96,8 +102,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   }
   const int b = s_item[0];
   if (b < 0) return;  // workgroup-uniform: past the last item
-  const int ctx = a.context_lens[b];
-  const int n_pages = (ctx + kPage - 1) / kPage;
+  const int ctx = min(a.context_lens[b], kPage * a.max_pages);
+  const int n_pages = attn_pages(ctx, a.max_pages);
   const int n_split = (n_pages + a.pps - 1) / a.pps;
   const int g = s_item[1] / n_split, split = s_item[1] % n_split;
   const int p_begin = split * a.pps;
@@ -261,8 +267,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 __global__ __launch_bounds__(128) void paged_attn_merge_kernel(AttnArgs a, uint16_t* __restrict__ out) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int G = a.Hq / a.Hkv, g = h / G, hh = h % G;
-  const int n_pages = (a.context_lens[b] + kPage - 1) / kPage;
+  const int n_pages = attn_pages(a.context_lens[b], a.max_pages);
   const int ns = (n_pages + a.pps - 1) / a.pps;
+  if (ns == 0) {  // an empty context attends to nothing
+    out[((long)b * a.Hq + h) * kHD + d] = 0;
+    return;
+  }
   const long base0 = ((long)b * a.Hkv + g) * a.max_splits * G + hh;
   float M = -INFINITY;
   for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base0 + (long)s * G) * 2]);
@@ -284,6 +294,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* __restri
                                                         const int32_t* __restrict__ positions, int Hkv, int max_pages) {
   const int b = blockIdx.x;
   const int pos = positions[b];
+  if (pos < 0 || pos >= kPage * max_pages) return;  // outside the block table: nothing to write
   const long pg = block_tables[(long)b * max_pages + pos / kPage];
   const int slot = pos % kPage;
   for (int i = threadIdx.x; i < Hkv * kHD; i += blockDim.x) {

@@ -84,7 +84,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   const uint16_t* src = qkv + ((long)b * nh + h) * kHD;
   float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
   const int pos = positions[b];
-  const long page = block_tables[(long)b * max_pages + pos / kPage];
+  // a position outside the block table has no page: q is still written, the cache is not
+  const bool in_table = pos >= 0 && pos < kPage * max_pages;
+  if (!in_table && h >= Hq) return;
+  const long page = in_table ? block_tables[(long)b * max_pages + pos / kPage] : 0;
   const int slot = pos % kPage;
   if (h >= Hq + Hkv) {  // v head: transposed page rows
     const int g = h - Hq - Hkv;

@@ -121,3 +121,43 @@ def test_paged_attention_rejects_bad_shapes(pkg, dev):
     t = torch.zeros((2, 2), dtype=torch.int32, device=dev)
     with pytest.raises(ValueError):
         pkg.paged_attention_decode(q, kc, vc, t, t[:, 0].contiguous(), 0.1)
+
+
+def test_paged_attention_out_of_table_contexts(pkg, dev):
+    """Context lengths are device data the host cannot check: a length past the block table
+    attends to the table's pages only, and an empty context gives zeros (never NaN, never a
+    read beyond the table)."""
+    rng = np.random.default_rng(12)
+    lens = [40, 70]
+    kc, vc, tables, seqs = build_cache(rng, lens, 4, poison=False)
+    tables = tables[:, :3]  # room for 48 tokens: the second sequence overflows it
+    q = orc.round_bf16(rng.standard_normal((3, 32, D)).astype(np.float32))
+    tab3 = np.concatenate([tables, tables[:1]], 0)
+    ctx = torch.tensor([40, 70, 0], dtype=torch.int32, device=dev)
+    out = pkg.paged_attention_decode(to_bf16(q, dev), to_bf16(kc, dev), to_bf16(vc, dev),
+                                     torch.from_numpy(np.ascontiguousarray(tab3)).to(dev), ctx, SCALE)
+    got = out.float().cpu().numpy()
+    k1, v1 = seqs[1]
+    ref = np.stack([att.decode_attention(q[0], *seqs[0], SCALE), att.decode_attention(q[1], k1[:48], v1[:48], SCALE)])
+    max_abs, mean_rel = errors(got[:2], ref)
+    assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
+    assert np.array_equal(got[2], np.zeros_like(got[2]))
+
+
+def test_kv_append_skips_positions_outside_the_table(pkg, dev):
+    rng = np.random.default_rng(13)
+    B, Hkv, n_pages = 3, 4, 5
+    kc = torch.zeros((n_pages, Hkv, PAGE, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((n_pages, Hkv, D, PAGE), dtype=torch.bfloat16, device=dev)
+    tables = np.array([[3, 1], [4, 2], [0, 1]], np.int32)
+    pos = np.array([20, -1, 32], np.int32)  # only the first is inside its 2-page table
+    k = orc.round_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32))
+    v = orc.round_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32))
+    pkg.kv_append(to_bf16(k, dev), to_bf16(v, dev), kc, vc, torch.from_numpy(tables).to(dev),
+                  torch.from_numpy(pos).to(dev))
+    torch.cuda.synchronize()
+    kcn, vcn = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+    expect_k, expect_v = np.zeros_like(kcn), np.zeros_like(vcn)
+    expect_k[1, :, 4, :] = k[0]
+    expect_v[1, :, :, 4] = v[0]
+    assert np.array_equal(kcn, expect_k) and np.array_equal(vcn, expect_v)

@@ -76,6 +76,31 @@ def test_qk_norm_rope_append(pkg, dev, Hq, Hkv, B):
         assert np.array_equal(vcn[pg, :, :, slot], heads[b, Hq + Hkv:])
 
 
+
+def test_qk_norm_rope_append_position_outside_the_table(pkg, dev):
+    """q is still produced; the cache is left untouched for a position with no page."""
+    from inference_server_amd import decode as dec
+
+    rng = np.random.default_rng(5)
+    Hq, Hkv, B = 4, 2, 2
+    nh = Hq + 2 * Hkv
+    qkv = orc.round_bf16(rng.standard_normal((B, nh * D)).astype(np.float32))
+    qw = orc.round_bf16((1 + 0.2 * rng.standard_normal(D)).astype(np.float32))
+    pos = np.array([40, 5], np.int32)  # the first is past its 2-page table
+    tables = np.array([[0, 1], [2, 3]], np.int32)
+    kc = torch.zeros((4, Hkv, PAGE, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros((4, Hkv, D, PAGE), dtype=torch.bfloat16, device=dev)
+    inv_freq = dec.default_inv_freq(dec.DecoderConfig(), dev)
+    q = pkg.qk_norm_rope_append(to_bf16(qkv, dev), to_bf16(qw, dev), to_bf16(qw, dev), inv_freq,
+                                torch.from_numpy(pos).to(dev), Hq, Hkv, 1e-6, kc, vc, torch.from_numpy(tables).to(dev))
+    torch.cuda.synchronize()
+    cos, sin = att.rope_cos_sin(pos, D, 1e6, inv_freq=inv_freq.cpu().numpy())
+    q_ref = att.rotary(att.rms_norm(qkv.reshape(B, nh, D)[:, :Hq], qw, 1e-6), cos, sin)
+    assert ulps(q.float().cpu().numpy(), q_ref).max() <= 1
+    kcn, vcn = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+    assert not kcn[[0, 1]].any() and not vcn[[0, 1]].any()  # sequence 0: nothing written
+    assert kcn[2, :, 5, :].any() and vcn[2, :, :, 5].any()  # sequence 1: its slot
+
 @pytest.mark.parametrize("T", [1, 64, 600])
 def test_moe_sublayer_equals_separate_calls(pkg, dev, T):
     E, H, I, k = 32, 512, 256, 4
