@@ -114,7 +114,7 @@ def test_route(pkg, dev, T, H, E, k):
 
 @pytest.mark.parametrize("T,k,E,block_m", [(1, 8, 128, 16), (16, 8, 128, 16), (64, 8, 128, 16),
                                            (512, 8, 128, 16), (513, 8, 128, 64), (4096, 8, 128, 64),
-                                           (3000, 4, 60, 32), (0, 8, 128, 16)])
+                                           (3000, 4, 60, 32), (4096, 8, 128, 256), (0, 8, 128, 16)])
 @pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
 def test_align_bit_exact(pkg, dev, T, k, E, block_m, index_dtype):
     rng = np.random.default_rng(5 + T)
