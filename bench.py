@@ -93,7 +93,7 @@ S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 #   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
 #                         --copy-probe                                 -> 291,674 / 25,447 KiB
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): 193412 * 1024 * 2 + 920 * 1024,
+    ("qwen3-30b-a3b", 64): 195244 * 1024 * 2 + 768 * 1024,
     ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
 }
 
