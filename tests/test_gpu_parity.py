@@ -303,3 +303,42 @@ def test_block_fused_quant_is_bit_exact(pkg, dev, w30b, router30b, T):
     out, (_, w, ids) = pkg.moe_block_fp8(x, router30b, 8, *w30b, return_routing=True)
     ref = pkg.experts_fp8(x, ids, w, *w30b)
     assert torch.equal(out, ref)
+
+
+# (T, H, I, E, k) chosen so that each GEMM tiling of the block runs (tile rows from S = T k:
+# 16 while S <= 8 E, 32 while S <= 16 E, then 128 when H % 256 == 0 and H, I >= 512, else 64),
+# with expert counts that are not powers of two, odd token counts and k = E.
+SHAPE_SWEEP = [
+    (5, 256, 128, 8, 2),       # 16-row tiles, 10 pairs
+    (1, 768, 256, 3, 3),       # k = E, one token
+    (30, 512, 256, 10, 4),     # 32-row tiles
+    (40, 384, 256, 6, 3),      # 64-row tiles (H % 256 != 0)
+    (77, 1024, 384, 20, 5),    # 64-row tiles (I < 512)
+    (300, 512, 512, 16, 4),    # 128-row prefill tiles, 4 K blocks per GEMM
+    (257, 1024, 640, 12, 6),   # 128-row prefill tiles, 5 K blocks in the down GEMM
+]
+
+
+@pytest.mark.parametrize("T,H,I,E,k", SHAPE_SWEEP)
+def test_block_shape_sweep(pkg, dev, T, H, I, E, k):
+    """Block output within the layer tolerance of the oracle on its own routing; routing
+    bit-exact given the kernel's logits; the experts path fed that routing reproduces the
+    block bit for bit."""
+    rng = np.random.default_rng(1000 + T + H + E)
+    x = orc.gen_normal_bf16(rng, (T, H))
+    wr = orc.gen_normal_bf16(rng, (E, H), 0.02)
+    w13 = orc.gen_normal_bf16(rng, (E, 2 * I, H), 0.02)
+    w2 = orc.gen_normal_bf16(rng, (E, H, I), 0.02)
+    q13, s13 = orc.quantize_weight_fp8(w13)
+    q2, s2 = orc.quantize_weight_fp8(w2)
+    dq13, ds13, dq2, ds2 = to_f8(q13, dev), to_dev(s13, dev), to_f8(q2, dev), to_dev(s2, dev)
+    xd = to_bf16(x, dev)
+    out, (lg, w, ids) = pkg.moe_block_fp8(xd, to_bf16(wr, dev), k, dq13, ds13, dq2, ds2, return_routing=True)
+    ids_ref, w_ref, _ = orc.topk_from_logits(np_f32(lg), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    assert bf16_ulp_diff(np_f32(w), w_ref).max() <= 1
+    ref = orc.experts_fp8(x, ids.cpu().numpy(), np_f32(w), q13, s13, q2, s2)
+    max_abs, mean_rel = errors(np_f32(out), ref)
+    assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
+    again = pkg.experts_fp8(xd, ids, w, dq13, ds13, dq2, ds2)
+    assert torch.equal(out, again)
