@@ -186,16 +186,18 @@ int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const 
                                    const int32_t* block_tables, int page_size, int max_pages, void* stream);
 
 /*
- * MoE sublayer of a decoder layer: out = h + moe_block(rms_norm(h, ln_weight)), with the
- * residual add done in the top-k combine.  Replaces Qwen3MoeDecoderLayer.forward's
- * TF/models/qwen3_moe/modeling_qwen3_moe.py:344-347 (post_attention_layernorm, the sparse
- * block :276-281, the residual add).  Arguments as moe_mi355x_block_fp8; ids int32.
+ * MoE sublayer of a decoder layer: out = h' + moe_block(rms_norm(h', ln_weight)) with
+ * h' = bf16(h + h_add) (h_add NULL: h' = h), the residual add done in the top-k combine.
+ * Replaces Qwen3MoeDecoderLayer.forward's TF/models/qwen3_moe/modeling_qwen3_moe.py:341-347
+ * (the residual add after the attention, post_attention_layernorm, the sparse block :276-281,
+ * the residual add).  h_add is the attention's o_proj output; other arguments as
+ * moe_mi355x_block_fp8.
  */
 size_t moe_mi355x_moe_sublayer_workspace_bytes(int T, int H, int I, int E, int k);
-int moe_mi355x_moe_sublayer_fp8(const void* h, const void* ln_weight, float eps, const void* w_router, int T,
-                                int H, int I, int E, int k, int renorm, const void* w13, const float* s13,
-                                const void* w2, const float* s2, void* out, void* workspace,
-                                size_t workspace_bytes, void* stream);
+int moe_mi355x_moe_sublayer_fp8(const void* h, const void* h_add, const void* ln_weight, float eps,
+                                const void* w_router, int T, int H, int I, int E, int k, int renorm,
+                                const void* w13, const float* s13, const void* w2, const float* s2, void* out,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Kernel timing (instrumentation; no counterpart in the reference).  While enabled, each

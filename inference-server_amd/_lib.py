@@ -44,8 +44,8 @@ SIGNATURES = {
     "moe_mi355x_qk_norm_rope_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                                 ctypes.c_float, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp]),
     "moe_mi355x_moe_sublayer_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
-    "moe_mi355x_moe_sublayer_fp8": (_c_int, [_vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                             _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "moe_mi355x_moe_sublayer_fp8": (_c_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "moe_mi355x_profile_enable": (_c_int, [_c_int]),
     "moe_mi355x_profile_read": (_c_int, [_c_int, ctypes.POINTER(_c_int), ctypes.POINTER(ctypes.c_double)]),
     "moe_mi355x_profile_slot_name": (ctypes.c_char_p, [_c_int]),

@@ -16,10 +16,13 @@ constexpr int kHD = 128;
 constexpr int kPage = 16;
 
 // y = bf16(w * bf16(x * r)), r = 1 / sqrt(sum(x^2) / C + eps): one wave per row, C <= 8192,
-// C % 8 == 0.  The row is read once into registers (16-byte loads).
+// C % 8 == 0.  The row is read once into registers (16-byte loads).  With `add` non-null the
+// normalised row is x = bf16(x + add) (the decoder layer's residual add before the
+// post-attention norm, modeling_qwen3_moe.py:341), also written to `sum_out` when non-null.
 template <int MAXV>  // uint4 chunks (8 values) per lane
-__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                       int R, int C, float eps, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ add,
+                                                       const uint16_t* __restrict__ w, int R, int C, float eps,
+                                                       uint16_t* __restrict__ out, uint16_t* __restrict__ sum_out) {
   // every product and sum below is rounded like the reference's separate torch ops: no
   // multiply-add contraction across the bf16 roundings
 #pragma clang fp contract(off)
@@ -33,6 +36,19 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restric
   for (int i = 0; i < MAXV; ++i) {
     const int c = (i * 64 + lane) * 8;
     v[i] = c < C ? *(const uint4*)(xr + c) : make_uint4(0, 0, 0, 0);
+    if (add != nullptr && c < C) {
+      const uint4 av = *(const uint4*)(add + (long)row * C + c);
+      const uint32_t xu[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, au[4] = {av.x, av.y, av.z, av.w};
+      uint32_t su[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = __uint_as_float(xu[j] << 16) + __uint_as_float(au[j] << 16);
+        const float hi = __uint_as_float(xu[j] & 0xffff0000u) + __uint_as_float(au[j] & 0xffff0000u);
+        su[j] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+      }
+      v[i] = make_uint4(su[0], su[1], su[2], su[3]);
+      if (sum_out != nullptr) *(uint4*)(sum_out + (long)row * C + c) = v[i];
+    }
     const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -119,19 +135,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
 
 }  // namespace
 
-int moe_launch_rms_norm(const void* x, const void* w, int R, int C, float eps, void* out, hipStream_t s) {
+int moe_launch_rms_norm(const void* x, const void* add, const void* w, int R, int C, float eps, void* out,
+                        void* sum_out, hipStream_t s) {
   if (R <= 0) return MOE_OK;
   const dim3 grid((R + 3) / 4), block(256);
   const int chunks = (C / 8 + 63) / 64;
   if (chunks <= 1)
-    hipLaunchKernelGGL((rms_norm_kernel<1>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)w, R, C, eps,
-                       (uint16_t*)out);
+    hipLaunchKernelGGL((rms_norm_kernel<1>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
+                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
   else if (chunks <= 4)
-    hipLaunchKernelGGL((rms_norm_kernel<4>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)w, R, C, eps,
-                       (uint16_t*)out);
+    hipLaunchKernelGGL((rms_norm_kernel<4>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
+                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
   else
-    hipLaunchKernelGGL((rms_norm_kernel<16>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)w, R, C, eps,
-                       (uint16_t*)out);
+    hipLaunchKernelGGL((rms_norm_kernel<16>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
+                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -142,7 +159,7 @@ extern "C" int moe_mi355x_rms_norm(const void* x, const void* weight, int rows, 
   if (rows == 0) return MOE_OK;
   MOE_RETURN_IF(!x || !weight || !out, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!moe_aligned16(x) || !moe_aligned16(weight) || !moe_aligned16(out), MOE_ERR_ALIGNMENT);
-  return moe_launch_rms_norm(x, weight, rows, cols, eps, out, (hipStream_t)stream);
+  return moe_launch_rms_norm(x, nullptr, weight, rows, cols, eps, out, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,

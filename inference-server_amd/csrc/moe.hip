@@ -294,30 +294,34 @@ extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, 
                     (hipStream_t)stream, nullptr);
 }
 
-int moe_launch_rms_norm(const void* x, const void* w, int R, int C, float eps, void* out, hipStream_t s);
+int moe_launch_rms_norm(const void* x, const void* add, const void* w, int R, int C, float eps, void* out,
+                        void* sum_out, hipStream_t s);
 
 extern "C" size_t moe_mi355x_moe_sublayer_workspace_bytes(int T, int H, int I, int E, int k) {
   if (!experts_args_ok(T, H, I, E, k, 4)) return 0;
-  return moe_align_up((size_t)T * H * 2, 256) + carve_block(nullptr, T, H, I, E, k).total;
+  return 2 * moe_align_up((size_t)T * H * 2, 256) + carve_block(nullptr, T, H, I, E, k).total;
 }
 
-extern "C" int moe_mi355x_moe_sublayer_fp8(const void* h, const void* ln_weight, float eps, const void* w_router,
-                                           int T, int H, int I, int E, int k, int renorm, const void* w13,
-                                           const float* s13, const void* w2, const float* s2, void* out,
-                                           void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int moe_mi355x_moe_sublayer_fp8(const void* h, const void* h_add, const void* ln_weight, float eps,
+                                           const void* w_router, int T, int H, int I, int E, int k, int renorm,
+                                           const void* w13, const float* s13, const void* w2, const float* s2,
+                                           void* out, void* workspace, size_t workspace_bytes, void* stream) {
   MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, 4), MOE_ERR_INVALID_ARG);
   if (T == 0) return MOE_OK;
   MOE_RETURN_IF(!h || !ln_weight || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
-  MOE_RETURN_IF(!experts_aligned(h, w13, w2, out) || !moe_aligned16(w_router) || !moe_aligned16(ln_weight),
+  MOE_RETURN_IF(!experts_aligned(h, w13, w2, out) || !moe_aligned16(w_router) || !moe_aligned16(ln_weight) ||
+                    (h_add && !moe_aligned16(h_add)),
                 MOE_ERR_ALIGNMENT);
   MOE_RETURN_IF(H > 8192, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_moe_sublayer_workspace_bytes(T, H, I, E, k),
                 MOE_ERR_WORKSPACE);
   hipStream_t s = (hipStream_t)stream;
-  void* xn = workspace;
-  const BlockWs b = carve_block((char*)workspace + moe_align_up((size_t)T * H * 2, 256), T, H, I, E, k);
-  int rc = moe_launch_rms_norm(h, ln_weight, T, H, eps, xn, s);
+  const size_t row_bytes = moe_align_up((size_t)T * H * 2, 256);
+  void* xn = workspace;                                 // the normalised rows
+  void* hs = (char*)workspace + row_bytes;              // bf16(h + h_add), the residual
+  const BlockWs b = carve_block((char*)workspace + 2 * row_bytes, T, H, I, E, k);
+  int rc = moe_launch_rms_norm(h, h_add, ln_weight, T, H, eps, xn, h_add ? hs : nullptr, s);
   if (rc) return rc;
   return block_impl(xn, w_router, T, H, I, E, k, renorm, w13, s13, w2, s2, out, nullptr, nullptr, 4, nullptr, b, s,
-                    h);
+                    h_add ? hs : h);
 }

@@ -12,11 +12,12 @@ server's model code, reached through TorchBackend's batched decode, torch_backen
     h = residual + o_proj(a)                                          (:189, :341)
     residual = h;  h = residual + moe_block(post_attention_layernorm(h))     (:344-347)
 
-Per layer this is seven launches of this library's HIP kernels plus three library calls:
+Per layer this is four entry points of this library plus two library GEMMs:
 ``moe_mi355x_rms_norm`` (input_layernorm), the fused q/k/v projection GEMM (hipBLASLt through
 torch), ``moe_mi355x_qk_norm_rope_append`` (q_norm, k_norm, rotary, KV-cache update),
-``moe_mi355x_paged_attn_decode``, the o_proj GEMM and the residual add (torch), and
-``moe_mi355x_moe_sublayer_fp8`` (post_attention_layernorm, the MoE block, the residual add).
+``moe_mi355x_paged_attn_decode``, the o_proj GEMM (torch), and ``moe_mi355x_moe_sublayer_fp8``
+(the residual add after the attention, post_attention_layernorm, the MoE block, the residual
+add).
 ``DecodeModel.capture`` records a whole step as one HIP graph, so a step costs one launch.
 """
 
@@ -116,8 +117,9 @@ class DecoderLayerWeights:
 
 def attention_sublayer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, inv_freq, k_cache,
                        v_cache):
-    """``h + o_proj(attention(input_layernorm(h)))`` for one new token per sequence, appending
-    the token's k, v to the cache (modeling_qwen3_moe.py:329-341 with :151-191)."""
+    """``o_proj(attention(input_layernorm(h)))`` for one new token per sequence, appending the
+    token's k, v to the cache (modeling_qwen3_moe.py:329-340 with :151-191).  The residual add
+    of :341 is left to the caller (the MoE sublayer forms it)."""
     cfg = w.cfg
     B = h.shape[0]
     x = kernels.rms_norm(h, w.ln1, cfg.rms_eps)
@@ -125,20 +127,21 @@ def attention_sublayer(w: DecoderLayerWeights, h, positions, context_lens, block
     q = kernels.qk_norm_rope_append(qkv, w.q_norm, w.k_norm, inv_freq, positions, cfg.heads, cfg.kv_heads,
                                     cfg.rms_eps, k_cache, v_cache, block_tables)
     a = kernels.paged_attention_decode(q, k_cache, v_cache, block_tables, context_lens, cfg.head_dim ** -0.5)
-    return h + torch.nn.functional.linear(a.view(B, cfg.heads * cfg.head_dim), w.wo)
+    return torch.nn.functional.linear(a.view(B, cfg.heads * cfg.head_dim), w.wo)
 
 
-def moe_sublayer(w: DecoderLayerWeights, h):
-    """``h + moe_block(post_attention_layernorm(h))`` (modeling_qwen3_moe.py:344-347)."""
+def moe_sublayer(w: DecoderLayerWeights, h, attn_out=None):
+    """``h' + moe_block(post_attention_layernorm(h'))`` with ``h' = h + attn_out``
+    (modeling_qwen3_moe.py:341-347; ``attn_out`` None: ``h' = h``)."""
     cfg = w.cfg
     return kernels.moe_sublayer_fp8(h, w.ln2, cfg.rms_eps, w.router, cfg.top_k, w.q13, w.s13, w.q2, w.s2,
-                                    norm_topk_prob=cfg.norm_topk_prob)
+                                    norm_topk_prob=cfg.norm_topk_prob, add=attn_out)
 
 
 def decoder_layer(w: DecoderLayerWeights, h, positions, context_lens, block_tables, inv_freq, k_cache, v_cache):
     """One full decoder layer for one decode step (modeling_qwen3_moe.py:319-348)."""
-    h = attention_sublayer(w, h, positions, context_lens, block_tables, inv_freq, k_cache, v_cache)
-    return moe_sublayer(w, h)
+    o = attention_sublayer(w, h, positions, context_lens, block_tables, inv_freq, k_cache, v_cache)
+    return moe_sublayer(w, h, o)
 
 
 class DecodeModel:
@@ -160,11 +163,14 @@ class DecodeModel:
 
     def step(self, h, positions, context_lens, block_tables, moe: bool = True, attention: bool = True):
         for i, w in enumerate(self.layers):
+            o = None
             if attention:
-                h = attention_sublayer(w, h, positions, context_lens, block_tables, self.inv_freq, self.cache.k[i],
+                o = attention_sublayer(w, h, positions, context_lens, block_tables, self.inv_freq, self.cache.k[i],
                                        self.cache.v[i])
             if moe:
-                h = moe_sublayer(w, h)
+                h = moe_sublayer(w, h, o)
+            elif o is not None:
+                h = h + o
         return h
 
     def capture(self, h, positions, context_lens, block_tables, moe: bool = True, attention: bool = True):

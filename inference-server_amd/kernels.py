@@ -369,12 +369,19 @@ def qk_norm_rope_append(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_w
 
 
 def moe_sublayer_fp8(hidden_states, ln_weight, eps, router_weight, top_k, gate_up_proj, gate_up_proj_scale_inv,
-                     down_proj, down_proj_scale_inv, norm_topk_prob: bool = True) -> torch.Tensor:
+                     down_proj, down_proj_scale_inv, norm_topk_prob: bool = True,
+                     add: torch.Tensor | None = None) -> torch.Tensor:
     """``h + moe_block(post_attention_layernorm(h))`` (modeling_qwen3_moe.py:344-347): the RMSNorm,
-    the MoE block and the residual add in one entry point."""
+    the MoE block and the residual add in one entry point.  With ``add`` (the attention's o_proj
+    output) the sublayer's input is ``h = bf16(hidden_states + add)``, the residual add of
+    :341, formed inside the RMSNorm and the combine instead of in a launch of its own."""
     _need(hidden_states, "hidden_states", torch.bfloat16, 2)
     _need(ln_weight, "ln_weight", torch.bfloat16, 1)
     _need(router_weight, "router_weight", torch.bfloat16, 2)
+    if add is not None:
+        _need(add, "add", torch.bfloat16, 2)
+        if add.shape != hidden_states.shape:
+            raise ValueError(f"add must match hidden_states {tuple(hidden_states.shape)}, got {tuple(add.shape)}")
     E, H, I = _check_expert_weights(gate_up_proj, gate_up_proj_scale_inv, down_proj, down_proj_scale_inv)
     T = hidden_states.shape[0]
     if hidden_states.shape[1] != H or tuple(router_weight.shape) != (E, H) or ln_weight.shape[0] != H:
@@ -383,8 +390,8 @@ def moe_sublayer_fp8(hidden_states, ln_weight, eps, router_weight, top_k, gate_u
     out = torch.empty_like(hidden_states)
     ws = _ws(lib.moe_mi355x_moe_sublayer_workspace_bytes(T, H, I, E, top_k), hidden_states.device)
     _lib.check(lib.moe_mi355x_moe_sublayer_fp8(
-        hidden_states.data_ptr(), ln_weight.data_ptr(), float(eps), router_weight.data_ptr(), T, H, I, E, top_k,
-        int(norm_topk_prob), gate_up_proj.data_ptr(), gate_up_proj_scale_inv.data_ptr(), down_proj.data_ptr(),
-        down_proj_scale_inv.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(hidden_states)),
-        "moe_sublayer_fp8")
+        hidden_states.data_ptr(), None if add is None else add.data_ptr(), ln_weight.data_ptr(), float(eps),
+        router_weight.data_ptr(), T, H, I, E, top_k, int(norm_topk_prob), gate_up_proj.data_ptr(),
+        gate_up_proj_scale_inv.data_ptr(), down_proj.data_ptr(), down_proj_scale_inv.data_ptr(), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), _stream(hidden_states)), "moe_sublayer_fp8")
     return out

@@ -114,3 +114,20 @@ def test_moe_sublayer_equals_separate_calls(pkg, dev, T):
     sep = h + pkg.moe_block_fp8(x, wr, k, q13, s13, q2, s2)
     torch.cuda.synchronize()
     assert torch.equal(fused, sep)
+
+
+@pytest.mark.parametrize("T", [1, 64, 600])
+def test_moe_sublayer_with_attention_residual(pkg, dev, T):
+    """With ``add`` the sublayer forms ``h' = bf16(h + add)`` itself (the residual add after the
+    attention): bit-identical to torch's bf16 add followed by the sublayer on ``h'``."""
+    E, H, I, k = 32, 512, 256, 4
+    q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=T + 1)
+    g = torch.Generator(device=dev).manual_seed(T + 1)
+    h = (torch.randn((T, H), generator=g, device=dev) * 2).to(torch.bfloat16)
+    o = (torch.randn((T, H), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    ln = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    fused = pkg.moe_sublayer_fp8(h, ln, 1e-6, wr, k, q13, s13, q2, s2, add=o)
+    sep = pkg.moe_sublayer_fp8(h + o, ln, 1e-6, wr, k, q13, s13, q2, s2)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, sep)
