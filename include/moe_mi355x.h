@@ -140,7 +140,8 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
  *   context_lens int32 [B]                  >= 1, <= 16 * max_pages (device data: a larger value
  *                                           is clamped to the table, 0 gives a zero output)
  * The KV layout is this library's; the reference keeps a contiguous per-layer cache.
- * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16.
+ * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16; q, k_cache,
+ * v_cache and out 16-byte aligned.
  */
 size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages);
 int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,

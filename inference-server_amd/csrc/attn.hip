@@ -263,27 +263,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   }
 }
 
-// out[b, h, :] = bf16( sum_s w_s O_s / sum_s w_s l_s ), w_s = exp(m_s - max m)
-__global__ __launch_bounds__(128) void paged_attn_merge_kernel(AttnArgs a, uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int G = a.Hq / a.Hkv, g = h / G, hh = h % G;
-  const int n_pages = attn_pages(a.context_lens[b], a.max_pages);
-  const int ns = (n_pages + a.pps - 1) / a.pps;
-  if (ns == 0) {  // an empty context attends to nothing
-    out[((long)b * a.Hq + h) * kHD + d] = 0;
-    return;
+// out[b, h, :] = bf16( sum_s w_s O_s / sum_s w_s l_s ), w_s = exp(m_s - max m), the sums in
+// split order.  One workgroup per (sequence, kv head); a thread owns 4 dims of one head of the
+// group.  The partials of the first kMergeUnroll splits are loaded at split indices clamped to
+// the workspace's max_splits (in bounds whatever the context length), in the same round trip
+// as the context length; splits past the sequence's count are masked.  Longer sequences (more
+// splits, small batches) continue in batches of kMergeUnroll.
+constexpr int kMergeUnroll = 8;
+__global__ __launch_bounds__(256) void paged_attn_merge_kernel(AttnArgs a, uint16_t* __restrict__ out) {
+  const int g = blockIdx.x, b = blockIdx.y;
+  const int G = a.Hq / a.Hkv;
+  const int ctx = a.context_lens[b];
+  for (int i = threadIdx.x; i < G * (kHD / 4); i += blockDim.x) {
+    const int hh = i / (kHD / 4), d0 = 4 * (i % (kHD / 4));
+    const long base0 = ((long)b * a.Hkv + g) * a.max_splits * G + hh;  // split s: base0 + s G
+    float2 ml[kMergeUnroll];
+    float4 ov[kMergeUnroll];
+    auto load = [&](int s0, int last) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        const long base = base0 + (long)min(s0 + u, last) * G;
+        ml[u] = *(const float2*)(a.part_ml + base * 2);
+        ov[u] = *(const float4*)(a.part_o + base * kHD + d0);
+      }
+    };
+    load(0, a.max_splits - 1);
+    uint16_t* dst = out + ((long)b * a.Hq + g * G + hh) * kHD + d0;
+    const int ns = (attn_pages(ctx, a.max_pages) + a.pps - 1) / a.pps;
+    if (ns == 0) {  // an empty context attends to nothing
+      *(uint2*)dst = make_uint2(0u, 0u);
+      continue;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) M = u < ns ? fmaxf(M, ml[u].x) : M;
+    for (int s0 = kMergeUnroll; s0 < ns; s0 += kMergeUnroll) {
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u)  // clamped repeats change no max
+        M = fmaxf(M, a.part_ml[(base0 + (long)min(s0 + u, ns - 1) * G) * 2]);
+    }
+    float L = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < ns; s0 += kMergeUnroll) {
+      if (s0 > 0) load(s0, ns - 1);
+#pragma unroll
+      for (int u = 0; u < kMergeUnroll; ++u) {
+        if (s0 + u >= ns) break;
+        const float w = __builtin_amdgcn_exp2f((ml[u].x - M) * 1.4426950408889634f);
+        L += ml[u].y * w;
+        acc[0] += ov[u].x * w;
+        acc[1] += ov[u].y * w;
+        acc[2] += ov[u].z * w;
+        acc[3] += ov[u].w * w;
+      }
+    }
+    *(uint2*)dst = make_uint2((uint32_t)f32_to_bf16(acc[0] / L) | ((uint32_t)f32_to_bf16(acc[1] / L) << 16),
+                              (uint32_t)f32_to_bf16(acc[2] / L) | ((uint32_t)f32_to_bf16(acc[3] / L) << 16));
   }
-  const long base0 = ((long)b * a.Hkv + g) * a.max_splits * G + hh;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, a.part_ml[(base0 + (long)s * G) * 2]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < ns; ++s) {
-    const long base = base0 + (long)s * G;
-    const float w = __builtin_amdgcn_exp2f((a.part_ml[base * 2] - M) * 1.4426950408889634f);
-    L += a.part_ml[base * 2 + 1] * w;
-    acc += a.part_o[base * kHD + d] * w;
-  }
-  out[((long)b * a.Hq + h) * kHD + d] = f32_to_bf16(acc / L);
 }
 
 // Writes the new token's k (row layout) and v (transposed layout) of every kv head at
@@ -335,7 +370,8 @@ extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, 
                                             void* stream) {
   MOE_RETURN_IF(!attn_args_ok(B, Hq, Hkv, head_dim, page_size, max_pages), MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!q || !k_cache || !v_cache || !block_tables || !context_lens || !out, MOE_ERR_INVALID_ARG);
-  MOE_RETURN_IF(!moe_aligned16(q) || !moe_aligned16(k_cache) || !moe_aligned16(v_cache), MOE_ERR_ALIGNMENT);
+  MOE_RETURN_IF(!moe_aligned16(q) || !moe_aligned16(k_cache) || !moe_aligned16(v_cache) || !moe_aligned16(out),
+                MOE_ERR_ALIGNMENT);
   MOE_RETURN_IF(!workspace || workspace_bytes < moe_mi355x_paged_attn_workspace_bytes(B, Hq, Hkv, max_pages),
                 MOE_ERR_WORKSPACE);
   const int pps = attn_pps(B, Hkv, max_pages);
@@ -350,7 +386,7 @@ extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, 
   // an upper bound of the (b, g, split) items; the kernel maps workgroups to the live ones
   hipLaunchKernelGGL(paged_attn_decode_kernel, dim3((unsigned)((long)B * Hkv * ms)), dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
-  hipLaunchKernelGGL(paged_attn_merge_kernel, dim3(Hq, B), dim3(kHD), 0, s, a, (uint16_t*)out);
+  hipLaunchKernelGGL(paged_attn_merge_kernel, dim3(Hkv, B), dim3(256), 0, s, a, (uint16_t*)out);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
