@@ -19,11 +19,14 @@
 // workgroups past the last one leave at once.  (A (split, head, sequence) grid whose empty
 // splits exit interleaved with the working ones reads the KV cache about 25% slower:
 // 4.5 against 5.8 TB/s in a loads-only model of this kernel, U[512, 8192] contexts.)  Per page a wave computes
-//   S^T [16 keys x 16 heads] = K [16 x 128] . Q^T [128 x 16]     (4 x mfma 16x16x32 bf16)
-//   O   [16 heads x 128]    += P [16 x 16 keys] . V [16 keys x 128] (8 x mfma 16x16x16 bf16)
-// where the query heads of the group fill rows 0..G-1 (G <= 16) and the rest are zero.  The
-// score tile's lane layout (lane l: keys 4 (l >> 4) + i of head l & 15) is exactly the A
-// operand layout of the second product, so P needs no shuffle.  Splits are combined by
+//   S^T [16 keys x 16 heads] = K [16 x 128] . Q^T [128 x 16]       (4 x mfma 16x16x32 bf16)
+//   O^T [128 x 16 heads]    += V^T [128 x 16 keys] . P^T [16 keys x 16 heads]
+//                                                                   (8 x mfma 16x16x16 bf16)
+// where the query heads of the group fill columns 0..G-1 (G <= 16) and the rest are zero.  The
+// score tile's lane layout (lane l: keys 4 (l >> 4) + i of head l & 15) is exactly the B
+// operand layout of the second product, so P needs no shuffle, and the output tile again
+// holds head l & 15 in lane l: the online-softmax rescale of a head is applied in the lanes
+// that hold its running max.  Splits are combined by
 // paged_attn_merge_kernel (log-sum-exp weights).
 #include "common.h"
 
@@ -36,6 +39,24 @@ constexpr int kPage = 16;       // tokens per page
 constexpr int kAttnWaves = 4;
 
 __device__ __forceinline__ float bf16_round(float f) { return (float)(__bf16)f; }
+
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the 16-lane rows of a wave) with
+// gfx950's row swaps: v_permlane16_swap exchanges rows 1 and 0, 3 and 2 between its two
+// operands, v_permlane32_swap the two halves, so combining the pair it returns gives every
+// lane op(own, partner) without an LDS permute.  The sums associate as (r0 + r1) + (r2 + r3)
+// in every lane.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // Pages of a context, clamped to the block table's width (context lengths are device data:
 // a value past the table would read beyond it).  Negative lengths count as empty.
@@ -176,8 +197,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       sv[i] = key0 + i < ctx ? x : -INFINITY;
     }
     float pm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    pm = fmaxf(pm, __shfl_xor(pm, 16));
-    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    pm = rows_max(pm);
     const float m_new = fmaxf(m_run, pm);  // finite: every page has at least one live key
     const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * 1.4426950408889634f);  // 0 on the first page
     float pv[4], ps = 0.f;
@@ -186,53 +206,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       pv[i] = __builtin_amdgcn_exp2f((sv[i] - m_new) * 1.4426950408889634f);
       ps += pv[i];
     }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = rows_sum(ps);
     l_run = l_run * corr + ps;
     m_run = m_new;
-    // P as the A operand (head lr, keys 4 lg + i)
-    v4s pa;
+    // P^T as the B operand (keys 4 lg + i of head lr)
+    v4s pb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pa[i] = (short)f32_to_bf16(pv[i]);
-    // rows of O in this lane are heads 4 lg + i: their correction factors live in lanes 4 lg + i
-    float cr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) cr[i] = __shfl(corr, 4 * lg + i);
+    for (int i = 0; i < 4; ++i) pb[i] = (short)f32_to_bf16(pv[i]);
     // keys past the end of the sequence (last page) have P = 0; their V slots may hold
-    // anything (the pool is not cleared), so they are zeroed rather than multiplied by 0
-    const int live_keys = ctx - key0;  // keys 4 lg + j with j < live_keys are valid
+    // anything (the pool is not cleared), so they are zeroed rather than multiplied by 0:
+    // keys 4 lg + j with j < live_keys are valid (j = 0, 1 in v.x, j = 2, 3 in v.y)
+    const int live_keys = ctx - key0;
+    const uint32_t mask_x = live_keys >= 2 ? 0xffffffffu : (live_keys == 1 ? 0xffffu : 0u);
+    const uint32_t mask_y = live_keys >= 4 ? 0xffffffffu : (live_keys == 3 ? 0xffffu : 0u);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      uint2 v = vr[n];
-      if (live_keys < 4) {
-        if (live_keys <= 0) v.x = v.y = 0u;
-        else if (live_keys == 1) { v.x &= 0xffffu; v.y = 0u; }
-        else if (live_keys == 2) v.y = 0u;
-        else v.y &= 0xffffu;
-      }
+      const uint32_t vx = vr[n].x & mask_x, vy = vr[n].y & mask_y;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[n][i] *= cr[i];
-      v4s vb;
-      vb[0] = (short)(v.x & 0xffffu);
-      vb[1] = (short)(v.x >> 16);
-      vb[2] = (short)(v.y & 0xffffu);
-      vb[3] = (short)(v.y >> 16);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[n], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) o[n][i] *= corr;
+      v4s va;  // V^T rows: dim 16 n + lr, keys 4 lg .. 4 lg + 3
+      va[0] = (short)(vx & 0xffffu);
+      va[1] = (short)(vx >> 16);
+      va[2] = (short)(vy & 0xffffu);
+      va[3] = (short)(vy >> 16);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[n], 0, 0, 0);
     }
     if (more) load_v(p + kAttnWaves);
   }
 
-  // merge the 4 waves: per head max, sum and O rows (heads 4 lg + i, dims 16 n + lr)
+  // merge the 4 waves: per head max, sum and O rows (head lr, dims 16 n + 4 lg + i)
   __shared__ float s_m[kAttnWaves][16], s_l[kAttnWaves][16];
-  __shared__ float s_o[kAttnWaves][16][kHD + 4];
+  __shared__ __attribute__((aligned(16))) float s_o[kAttnWaves][16][kHD + 4];
   if (lg == 0) {
     s_m[wave][lr] = m_run;
     s_l[wave][lr] = l_run;
   }
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s_o[wave][4 * lg + i][16 * n + lr] = o[n][i];
+  for (int n = 0; n < 8; ++n) *(v4f*)&s_o[wave][lr][16 * n + 4 * lg] = o[n];
   __syncthreads();
   // 256 threads: head hh = tid / 16 (< G used), dims 8 (tid % 16) .. +8
   const int hh = threadIdx.x >> 4, d0 = (threadIdx.x & 15) * 8;
