@@ -6,6 +6,7 @@ Importable as ``inference_server_amd`` (the on-disk folder name carries a hyphen
 Layers:
   ``_lib``     ctypes binding of ``libmoe_mi355x.so`` (C ABI: ``include/moe_mi355x.h``)
   ``kernels``  torch-tensor wrappers of every entry point
+  ``torch_ops`` the route / align / moe_fp8 / moe_block_fp8 entry points as ``torch.ops.moe_mi355x``
   ``experts``  drop-in modules, the transformers experts-interface registration, and the
                HIP-graph replay of a block per decode batch bucket
   ``checkpoint`` FP8 expert layers from a local safetensors checkpoint
@@ -14,7 +15,7 @@ Layers:
 
 from __future__ import annotations
 
-from . import _lib, decode, kernels  # noqa: F401
+from . import _lib, decode, kernels, torch_ops  # noqa: F401
 from .checkpoint import CheckpointIndex, load_moe_block, load_moe_layer  # noqa: F401
 from .experts import (  # noqa: F401
     IMPLEMENTATION_KEY,

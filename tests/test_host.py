@@ -70,3 +70,42 @@ def test_swap_finds_qwen3_moe_blocks(pkg, monkeypatch):
     assert pkg.swap_moe_blocks(model) == 2
     assert len(seen) == 2
     assert all(isinstance(layer.mlp, torch.nn.Identity) for layer in model.model.layers)
+
+
+def test_torch_ops_are_registered(pkg):
+    ops = torch.ops.moe_mi355x
+    for name in ("route", "align", "moe_fp8", "moe_block_fp8"):
+        assert hasattr(ops, name), name
+    pkg.torch_ops.register()  # a second registration in the same process is a no-op
+
+
+def test_torch_ops_fake_shapes(pkg):
+    """The operators' fake implementations (meta tensors: no device, no library call) give
+    the shapes and dtypes of the real outputs."""
+    T, H, I, E, k = 5, 256, 128, 16, 4
+    m = dict(device="meta")
+    x = torch.empty((T, H), dtype=torch.bfloat16, **m)
+    wr = torch.empty((E, H), dtype=torch.bfloat16, **m)
+    ids, w, logits = torch.ops.moe_mi355x.route(x, wr, k, True)
+    assert (ids.shape, ids.dtype, w.shape, w.dtype, logits.shape) == ((T, k), torch.int32, (T, k), torch.bfloat16,
+                                                                       (T, E))
+    perm, tiles, counts, offsets, n_tiles = torch.ops.moe_mi355x.align(ids, E, 16)
+    assert perm.shape == (T * k,) and counts.shape == (E,) and offsets.shape == (E + 1,) and n_tiles.shape == (1,)
+    assert tiles.shape == (pkg.torch_ops.align_max_tiles(T * k, E, 16), 4)
+    fp8 = torch.float8_e4m3fn
+    w13 = torch.empty((E, 2 * I, H), dtype=fp8, **m)
+    s13 = torch.empty((E, 2 * I // 128, H // 128), dtype=torch.float32, **m)
+    w2 = torch.empty((E, H, I), dtype=fp8, **m)
+    s2 = torch.empty((E, H // 128, I // 128), dtype=torch.float32, **m)
+    assert torch.ops.moe_mi355x.moe_fp8(x, ids, w, w13, s13, w2, s2).shape == (T, H)
+    x3 = torch.empty((2, 3, H), dtype=torch.bfloat16, **m)
+    out = torch.ops.moe_mi355x.moe_block_fp8(x3, wr, k, True, w13, s13, w2, s2)
+    assert out.shape == (2, 3, H) and out.dtype == torch.bfloat16
+
+
+def test_align_max_tiles_matches_library(pkg):
+    lib = pkg._lib.load()
+    for S in (0, 1, 7, 8, 64, 512, 1000, 32768):
+        for E in (1, 8, 128):
+            for bm in (16, 32, 128):
+                assert pkg.torch_ops.align_max_tiles(S, E, bm) == max(lib.moe_mi355x_align_max_tiles(S, E, bm), 1)
