@@ -64,3 +64,18 @@ def test_opcheck(pkg, dev):
         after = [a.view(torch.uint8) for a in args if isinstance(a, torch.Tensor)]
         assert all(torch.equal(u, v) for u, v in zip(before, after)), name
     torch.cuda.synchronize()
+
+
+def test_ops_trace_under_compile(pkg, dev):
+    """A function around the block operator compiles with fullgraph=True (the fake
+    implementation drives the trace; aot_eager runs the traced graph without codegen) and
+    returns the eager result."""
+    x, wr = _inputs(dev, 24, seed=2)
+    q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=2)
+
+    def layer(h):
+        return h + torch.ops.moe_mi355x.moe_block_fp8(h, wr, K, True, q13, s13, q2, s2)
+
+    compiled = torch.compile(layer, backend="aot_eager", fullgraph=True)
+    assert torch.equal(compiled(x), layer(x))
+    torch.cuda.synchronize()
