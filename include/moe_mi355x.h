@@ -136,7 +136,9 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
  *   q            bf16 [B, Hq, 128]          out bf16 [B, Hq, 128]
  *   k_cache      bf16 [pages, Hkv, 16, 128] (token rows)
  *   v_cache      bf16 [pages, Hkv, 128, 16] (transposed: dim rows)
- *   block_tables int32 [B, max_pages]       page of each 16-token block of a sequence
+ *   block_tables int32 [B, max_pages]       page of each 16-token block of a sequence (device
+ *                                           data, not checked: the entries a context covers must
+ *                                           be page indices of the pools)
  *   context_lens int32 [B]                  >= 1, <= 16 * max_pages (device data: a larger value
  *                                           is clamped to the table, 0 gives a zero output)
  * The KV layout is this library's; the reference keeps a contiguous per-layer cache.

@@ -150,7 +150,8 @@ class DecodeModel:
     ``step(h, positions, context_lens, block_tables)`` runs every layer on the hidden states of
     the batch's new tokens ([B, hidden] bf16; ``positions`` int32 [B] = index of the new token,
     ``context_lens`` = positions + 1, ``block_tables`` int32 [B, max_pages]).  ``capture`` records
-    one step as a HIP graph over static input buffers; ``replay`` runs it.
+    one step as a HIP graph over static input buffers: copy a step's inputs into those buffers,
+    then call the graph's ``replay()``.
     """
 
     def __init__(self, cfg: DecoderConfig, layers: list[DecoderLayerWeights], cache: PagedKVCache):

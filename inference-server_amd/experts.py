@@ -143,15 +143,13 @@ class MI355XSparseMoeBlock(nn.Module):
         E, H = gate.weight.shape
         renorm = gate.norm_topk_prob if norm_topk_prob is None else norm_topk_prob
         dev = gate.weight.device
+        I = experts.gate_up_proj.shape[1] // 2
+        new = cls(E, H, I, gate.top_k, renorm, device=dev)
         if experts.gate_up_proj.dtype == torch.float8_e4m3fn:
-            I = experts.gate_up_proj.shape[1] // 2
-            new = cls(E, H, I, gate.top_k, renorm, device=dev)
             with torch.no_grad():
                 for name in ("gate_up_proj", "gate_up_proj_scale_inv", "down_proj", "down_proj_scale_inv"):
                     getattr(new.experts, name).copy_(getattr(experts, name))
         else:
-            I = experts.gate_up_proj.shape[1] // 2
-            new = cls(E, H, I, gate.top_k, renorm, device=dev)
             new.experts = MI355XFp8Experts.from_bf16(experts.gate_up_proj.detach(), experts.down_proj.detach())
         with torch.no_grad():
             new.gate.weight.copy_(gate.weight.to(torch.bfloat16))
@@ -187,8 +185,10 @@ class MI355XGraphedMoeBlock(nn.Module):
     once per bucket size (the smallest bucket >= the batch; batches are zero-padded up to it, and
     the padded rows' outputs are dropped) and replays the graph afterwards.  Batches above the
     largest bucket run eagerly.  Inputs are copied into the graph's static buffer, so the caller's
-    tensors may live anywhere.  Graphs are captured on first use of a bucket; ``capture()``
-    captures them up front.
+    tensors may live anywhere.  The output (bf16 inputs) is a view of the graph's static output
+    buffer, valid until this module's next call: clone it to keep it longer (the decoder layer
+    consumes it at once in its residual add, modeling_qwen3_moe.py:347).  Graphs are captured on
+    first use of a bucket; ``capture()`` captures them up front.
     """
 
     def __init__(self, block: MI355XSparseMoeBlock, buckets=(1, 2, 4, 8, 16, 32, 64, 128, 256)):

@@ -267,6 +267,16 @@ PAGE_SIZE = 16
 HEAD_DIM = 128
 
 
+def _check_kv_pools(k_cache: torch.Tensor, v_cache: torch.Tensor, num_kv_heads: int) -> None:
+    """K pool [pages, Hkv, 16, 128] and V pool [pages, Hkv, 128, 16] of the same size (the
+    kernels index both by the same page id)."""
+    P = k_cache.shape[0]
+    if tuple(k_cache.shape) != (P, num_kv_heads, PAGE_SIZE, HEAD_DIM):
+        raise ValueError(f"k_cache must be [pages, {num_kv_heads}, {PAGE_SIZE}, {HEAD_DIM}], got {tuple(k_cache.shape)}")
+    if tuple(v_cache.shape) != (P, num_kv_heads, HEAD_DIM, PAGE_SIZE):
+        raise ValueError(f"v_cache must be [{P}, {num_kv_heads}, {HEAD_DIM}, {PAGE_SIZE}], got {tuple(v_cache.shape)}")
+
+
 def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float) -> torch.Tensor:
     """Decode attention of one new token per sequence over a paged KV cache.
@@ -314,8 +324,11 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     _need(block_tables, "block_tables", torch.int32, 2)
     _need(positions, "positions", torch.int32, 1)
     B, Hkv, D = k.shape
-    if tuple(v.shape) != (B, Hkv, D) or D != HEAD_DIM or k_cache.shape[1] != Hkv:
-        raise ValueError("k, v must be [B, Hkv, 128] matching the cache's kv heads")
+    if tuple(v.shape) != (B, Hkv, D) or D != HEAD_DIM:
+        raise ValueError("k, v must be [B, Hkv, 128]")
+    _check_kv_pools(k_cache, v_cache, Hkv)
+    if block_tables.shape[0] != B or positions.shape[0] != B:
+        raise ValueError("block_tables and positions need one row per sequence")
     _lib.check(_lib.load().moe_mi355x_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                                 block_tables.data_ptr(), positions.data_ptr(), B, Hkv, HEAD_DIM,
                                                 PAGE_SIZE, block_tables.shape[1], _stream(k)), "kv_append")
@@ -358,8 +371,9 @@ def qk_norm_rope_append(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_w
     B = qkv.shape[0]
     if qkv.shape[1] != (num_heads + 2 * num_kv_heads) * HEAD_DIM or inv_freq.shape[0] != HEAD_DIM // 2:
         raise ValueError("qkv must be [B, (Hq + 2 Hkv) * 128] and inv_freq [64]")
-    if k_cache.shape[1] != num_kv_heads or positions.shape[0] != B or block_tables.shape[0] != B:
-        raise ValueError("cache kv heads, positions and block tables must match the batch")
+    _check_kv_pools(k_cache, v_cache, num_kv_heads)
+    if positions.shape[0] != B or block_tables.shape[0] != B:
+        raise ValueError("positions and block tables must match the batch")
     q = torch.empty((B, num_heads, HEAD_DIM), dtype=torch.bfloat16, device=qkv.device)
     _lib.check(_lib.load().moe_mi355x_qk_norm_rope_append(
         qkv.data_ptr(), q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), inv_freq.data_ptr(), positions.data_ptr(),
@@ -383,6 +397,8 @@ def moe_sublayer_fp8(hidden_states, ln_weight, eps, router_weight, top_k, gate_u
         if add.shape != hidden_states.shape:
             raise ValueError(f"add must match hidden_states {tuple(hidden_states.shape)}, got {tuple(add.shape)}")
     E, H, I = _check_expert_weights(gate_up_proj, gate_up_proj_scale_inv, down_proj, down_proj_scale_inv)
+    if not 1 <= top_k <= min(E, 32):
+        raise ValueError("top_k must be in [1, min(E, 32)]")
     T = hidden_states.shape[0]
     if hidden_states.shape[1] != H or tuple(router_weight.shape) != (E, H) or ln_weight.shape[0] != H:
         raise ValueError("hidden_states, ln_weight and router_weight must match the experts' hidden size")

@@ -123,6 +123,25 @@ def test_paged_attention_rejects_bad_shapes(pkg, dev):
         pkg.paged_attention_decode(q, kc, vc, t, t[:, 0].contiguous(), 0.1)
 
 
+def test_cache_writers_reject_mismatched_pools(pkg, dev):
+    """A V pool that is not the K pool's [pages, Hkv, 128, 16] counterpart is refused before
+    any kernel could write past it."""
+    kc = torch.zeros((4, 2, PAGE, D), dtype=torch.bfloat16, device=dev)
+    bad_v = [torch.zeros((2, 2, D, PAGE), dtype=torch.bfloat16, device=dev),   # fewer pages
+             torch.zeros((4, 2, PAGE, D), dtype=torch.bfloat16, device=dev)]   # K's layout
+    k = torch.zeros((1, 2, D), dtype=torch.bfloat16, device=dev)
+    t = torch.zeros((1, 4), dtype=torch.int32, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    qkv = torch.zeros((1, 8 * D), dtype=torch.bfloat16, device=dev)
+    nw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    inv = torch.ones(D // 2, dtype=torch.float32, device=dev)
+    for vc in bad_v:
+        with pytest.raises(ValueError, match="v_cache"):
+            pkg.kv_append(k, k, kc, vc, t, pos)
+        with pytest.raises(ValueError, match="v_cache"):
+            pkg.qk_norm_rope_append(qkv, nw, nw, inv, pos, 4, 2, 1e-6, kc, vc, t)
+
+
 def test_paged_attention_out_of_table_contexts(pkg, dev):
     """Context lengths are device data the host cannot check: a length past the block table
     attends to the table's pages only, and an empty context gives zeros (never NaN, never a
