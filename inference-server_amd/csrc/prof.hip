@@ -4,6 +4,7 @@
 // recorded on the launch stream; moe_mi355x_profile_read() synchronises those events
 // and returns count and summed duration per kernel slot.  Disabled (the default), the
 // brackets cost one branch.  Host-side only; thread-safe.
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -17,7 +18,7 @@ struct Rec {
 };
 
 std::mutex g_mu;
-bool g_enabled = false;
+std::atomic<bool> g_enabled{false};  // read on every launch without taking the lock
 std::vector<Rec> g_recs;
 std::vector<hipEvent_t> g_free;
 
@@ -43,7 +44,7 @@ void recycle_all() {
 }  // namespace
 
 int moe_prof_begin(int slot, hipStream_t s) {
-  if (!g_enabled) return -1;
+  if (!g_enabled.load(std::memory_order_relaxed)) return -1;
   std::lock_guard<std::mutex> lk(g_mu);
   Rec r{slot, take_event(), take_event()};
   if (!r.a || !r.b) return -1;
@@ -61,7 +62,7 @@ void moe_prof_end(int id, hipStream_t s) {
 extern "C" int moe_mi355x_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(g_mu);
   recycle_all();
-  g_enabled = on != 0;
+  g_enabled.store(on != 0, std::memory_order_relaxed);
   return MOE_OK;
 }
 
