@@ -46,7 +46,10 @@ constexpr int kMaxKB = 32;  // K <= 4096
 
 // DN: 16-column slices per wave in the down GEMM (adjacent), so that a wave streams as
 // many weight bytes per setup as a gate_up wave (which pairs a gate and an up slice).
-template <int MODE, int WM, int KS, int DN = 1>
+// SHA (32-row tiles, no K split): the tile's activation K block is staged once per workgroup in
+// LDS and every column wave reads its fragments there, instead of each wave loading the same
+// rows from memory (the four column waves would put 4x the activation bytes through L1).
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
 __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
   constexpr int NOP = MODE == MODE_GATE_UP ? 2 : DN;  // B operands per wave (gate, up | column slices)
@@ -68,6 +71,11 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   __shared__ int s_arow[BM];                 // activation row of each tile row
   __shared__ float s_sa[BM][kMaxKB];         // activation scales of the tile
   __shared__ float s_red[KS > 1 ? (KS - 1) * CG * WM * NOP * 4 * 64 : 1];
+  // SHA: two K blocks of the tile's activations, 8 16-byte chunks per row; chunk c of row r at
+  // c ^ (r & 7), so that the 16-row fragment reads (one chunk column per 16 lanes) are
+  // conflict-free
+  __shared__ __attribute__((aligned(16))) uint4 s_at[SHA ? 2 : 1][SHA ? BM * 8 : 1];
+  static_assert(!SHA || (KS == 1 && BM * 8 == 256), "SHA stages one 16-byte chunk per thread, no K split");
 
   // The weight stream needs only the expert and the column block: its first loads go
   // out before the activation-row setup (perm -> rows -> scales), whose dependent round
@@ -98,30 +106,14 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
   __syncthreads();
 
-  const uint8_t* aptr[WM];
-#pragma unroll
-  for (int mi = 0; mi < WM; ++mi) aptr[mi] = p.a + (long)s_arow[mi * 16 + lr] * p.K + lg * 32;
   v4f acc[WM][NOP];
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi)
 #pragma unroll
     for (int o = 0; o < NOP; ++o) acc[mi][o] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  v8i ac[WM];
-  int kb = ks;
-  if (kb < KB) {
-#pragma unroll
-    for (int mi = 0; mi < WM; ++mi) ac[mi] = *(const v8i*)(aptr[mi] + kb * MOE_GROUP);
-  }
-  for (; kb < KB; kb += KS) {
-    v8i bn[NOP], an[WM];
-    const int kn = kb + KS;
-    if (kn < KB) {
-#pragma unroll
-      for (int o = 0; o < NOP; ++o) bn[o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
-#pragma unroll
-      for (int mi = 0; mi < WM; ++mi) an[mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
-    }
+  // the MFMAs of K block kb on activation fragments a and weight fragments bc
+  auto mfma_block = [&](const v8i (&a)[WM], int kb) __attribute__((always_inline)) {
     float swv[NOP];
 #pragma unroll
     for (int o = 0; o < NOP; ++o) swv[o] = swp[o][kb];
@@ -133,16 +125,74 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
       for (int o = 0; o < NOP; ++o) {
         const v4f zero = {0.f, 0.f, 0.f, 0.f};
-        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ac[mi], bc[o], zero, 0, 0, 0, 0, 0, 0);
+        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bc[o], zero, 0, 0, 0, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[mi][o][q] = fmaf(t[q], sav[q] * swv[o], acc[mi][o][q]);
       }
     }
-    if (kn < KB) {
+  };
+
+  if constexpr (SHA) {
+    // thread t stages chunk t & 7 of tile row t >> 3: K block kb + 1 is loaded into a register
+    // while kb is computed and stored to the other LDS buffer after the MFMAs; one barrier per
+    // K block
+    const int sr = threadIdx.x >> 3, sc = threadIdx.x & 7;
+    const uint8_t* sptr = p.a + (long)s_arow[sr] * p.K + sc * 16;
+    const int sidx = sr * 8 + (sc ^ (sr & 7));
+    s_at[0][sidx] = *(const uint4*)sptr;
+    uint4 ra = *(const uint4*)(sptr + (long)min(1, KB - 1) * MOE_GROUP);
+    __syncthreads();
+    for (int kb = 0; kb < KB; ++kb) {
+      v8i bn[NOP];
+      const int kn = kb + 1;
+      if (kn < KB) {
 #pragma unroll
-      for (int o = 0; o < NOP; ++o) bc[o] = bn[o];
+        for (int o = 0; o < NOP; ++o) bn[o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
+      }
+      // fragment of row mi * 16 + lr: its chunks 2 lg and 2 lg + 1
+      v8i af[WM];
 #pragma unroll
-      for (int mi = 0; mi < WM; ++mi) ac[mi] = an[mi];
+      for (int mi = 0; mi < WM; ++mi) {
+        const int r = mi * 16 + lr;
+        const uint4 lo = s_at[kb & 1][r * 8 + ((2 * lg) ^ (r & 7))];
+        const uint4 hi = s_at[kb & 1][r * 8 + ((2 * lg + 1) ^ (r & 7))];
+        af[mi] = (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+      mfma_block(af, kb);
+      if (kn < KB) {
+        s_at[kn & 1][sidx] = ra;
+        ra = *(const uint4*)(sptr + (long)min(kn + 1, KB - 1) * MOE_GROUP);
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) bc[o] = bn[o];
+      }
+      __syncthreads();  // block kn visible, and every wave done with buffer kb & 1
+    }
+  } else {
+    const uint8_t* aptr[WM];
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi) aptr[mi] = p.a + (long)s_arow[mi * 16 + lr] * p.K + lg * 32;
+    v8i ac[WM];
+    int kb = ks;
+    if (kb < KB) {
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi) ac[mi] = *(const v8i*)(aptr[mi] + kb * MOE_GROUP);
+    }
+    for (; kb < KB; kb += KS) {
+      v8i bn[NOP], an[WM];
+      const int kn = kb + KS;
+      if (kn < KB) {
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) bn[o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi) an[mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
+      }
+      mfma_block(ac, kb);
+      if (kn < KB) {
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) bc[o] = bn[o];
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi) ac[mi] = an[mi];
+      }
     }
   }
 
@@ -192,7 +242,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
 }
 
-template <int MODE, int WM, int KS, int DN = 1>
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;
@@ -200,7 +250,7 @@ int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   // come after every working one instead of between them, and consecutive workgroups stream
   // adjacent weight rows of one expert (gate_up at 64 tokens 75 -> 70 us)
   dim3 grid(a.N / (WCOLS * CG), max_tiles);
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN>),
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA>),
              grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -238,7 +288,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   if (block_m == 16)
     rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
   else if (block_m == 32)  // no K split: 64 h columns per workgroup share one load of the tile's rows
-    rc = launch_gemm<MODE_GATE_UP, 2, 1>(g1, max_tiles, s);
+    rc = launch_gemm<MODE_GATE_UP, 2, 1, 1, true>(g1, max_tiles, s);
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
@@ -250,7 +300,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
     rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
   else if (block_m == 32)
-    rc = launch_gemm<MODE_DOWN, 2, 1, 2>(g2, max_tiles, s);
+    rc = launch_gemm<MODE_DOWN, 2, 1, 2, true>(g2, max_tiles, s);
   else
     rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
   return rc;
