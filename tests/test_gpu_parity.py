@@ -321,6 +321,8 @@ SHAPE_SWEEP = [
     (77, 1024, 384, 20, 5),    # 64-row tiles (I < 512)
     (300, 512, 512, 16, 4),    # 128-row prefill tiles, 4 K blocks per GEMM
     (257, 1024, 640, 12, 6),   # 128-row prefill tiles, 5 K blocks in the down GEMM
+    (24, 256, 4096, 2, 1),     # the largest intermediate size: 32 K blocks in the down GEMM
+    (600, 512, 4096, 4, 2),    # the same on the 128-row prefill tiles
 ]
 
 
