@@ -48,47 +48,7 @@ __global__ __launch_bounds__(kChunk) void align_count_kernel(const void* ids, in
   for (int e = threadIdx.x; e <= E; e += blockDim.x) bc[(long)blockIdx.x * (E + 1) + e] = s_cnt[e];
 }
 
-// Large S, pass 2 (one workgroup): totals, offsets, tile list, and each chunk's
-// starting slot per expert, written back over bc.  The chunk histograms are staged in
-// LDS when they fit (every per-expert walk over the chunks then reads LDS, not global
-// memory with one round trip per chunk).
-constexpr int kScanLds = 16384;  // ints of staged histograms (64 KB)
-__global__ __launch_bounds__(kChunk) void align_scan_kernel(int32_t* bc, int nb, int E, int block_m,
-                                                            int32_t* counts, int32_t* offsets, int32_t* tiles,
-                                                            int32_t* n_tiles) {
-  __shared__ int s_cnt[kBuckets];
-  __shared__ int s_off[kBuckets];
-  __shared__ int s_toff[kBuckets];
-  __shared__ int s_bc[kScanLds];
-  const int n = nb * (E + 1);
-  const bool staged = n <= kScanLds;  // workgroup-uniform
-  if (staged) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) s_bc[i] = bc[i];
-    __syncthreads();
-  }
-  const int32_t* src = staged ? s_bc : bc;
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    int tot = 0;
-#pragma unroll 8
-    for (int b = 0; b < nb; ++b) tot += src[(long)b * (E + 1) + e];
-    s_cnt[e] = tot;
-  }
-  __syncthreads();
-  scan_counts(s_cnt, E, block_m, s_off, s_toff);
-  __syncthreads();
-  emit_meta(s_cnt, s_off, s_toff, E, block_m, counts, offsets, tiles, n_tiles);
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    int run = s_off[e];
-#pragma unroll 8
-    for (int b = 0; b < nb; ++b) {
-      const int c = src[(long)b * (E + 1) + e];
-      bc[(long)b * (E + 1) + e] = run;
-      run += c;
-    }
-  }
-}
-
-// Large S, passes 2 + 3 in one launch: every workgroup reduces all chunk histograms (its
+// Large S, pass 2 (one launch): every workgroup reduces all chunk histograms (its
 // chunk's starting slot per expert = offset of the expert + counts of the earlier chunks),
 // workgroup 0 writes counts, offsets and the tile list, and each places its chunk stably.
 __global__ __launch_bounds__(kChunk) void align_scan_scatter_kernel(const void* ids, int id_bytes, int S, int E,
@@ -120,16 +80,6 @@ __global__ __launch_bounds__(kChunk) void align_scan_scatter_kernel(const void* 
   for (int e = threadIdx.x; e <= E; e += blockDim.x) s_base[e] += s_off[e];
   __syncthreads();
   scatter_chunk(ids, id_bytes, S, E, b * kChunk, s_base, s_wcnt, perm);
-}
-
-// Large S, pass 3: stable placement of chunk b starting from its per-expert slots.
-__global__ __launch_bounds__(kChunk) void align_scatter_kernel(const void* ids, int id_bytes, int S, int E,
-                                                               const int32_t* bases, int32_t* perm) {
-  __shared__ int s_base[kBuckets];
-  __shared__ int s_wcnt[kWaves][kBuckets];
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) s_base[e] = bases[(long)blockIdx.x * (E + 1) + e];
-  __syncthreads();
-  scatter_chunk(ids, id_bytes, S, E, blockIdx.x * kChunk, s_base, s_wcnt, perm);
 }
 
 }  // namespace
