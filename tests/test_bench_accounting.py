@@ -1,0 +1,58 @@
+"""bench.py's roofline accounting against the figures derived independently from the layer
+shapes (bytes per active expert, algorithmic flops, expected active experts, path choice), so
+that a slip in a formula shows here and not as a wrong fraction in the report."""
+
+from __future__ import annotations
+
+import pytest
+
+import bench
+
+
+def test_bytes_per_expert_30b():
+    s = bench.S30B
+    # W13: 2 * 768 * 2048 e4m3 bytes + 12 * 16 fp32 scales; W2: 2048 * 768 + 16 * 6 scales
+    assert s.gate_up_expert_bytes() == 2 * 768 * 2048 + 4 * 12 * 16 == 3_146_496
+    assert s.expert_bytes() == 3_146_496 + 2048 * 768 + 4 * 16 * 6 == 4_719_744
+
+
+def test_bytes_per_expert_235b():
+    s = bench.S235B
+    assert s.expert_bytes() == 3 * 4096 * 1536 + 4 * (24 * 32 + 32 * 12) == 18_878_976
+
+
+def test_gate_up_bytes_and_flops():
+    s = bench.S30B
+    # activations in (fp8 + scales) and the bf16 intermediate out, on top of the weights
+    assert s.gate_up_bytes(10, 64) == 10 * 3_146_496 + 64 * 2048 + 4 * 64 * 16 + 2 * 64 * 8 * 768
+    assert s.gate_up_flops(4096) == 2 * 4096 * 8 * 1536 * 2048
+    # the whole layer at a 4096-token chunk: 9,437,184 flop per pair + the router
+    assert s.layer_flops(4096) == pytest.approx(4096 * 8 * 9_437_184 + 4096 * 2 * 2048 * 128)
+    assert s.layer_flops(4096) == pytest.approx(3.114e11, rel=1e-3)
+
+
+@pytest.mark.parametrize("T,expected", [(1, 8.0), (8, 51.6), (32, 111.8), (64, 125.9), (128, 128.0)])
+def test_expected_active_experts(T, expected):
+    assert bench.S30B.expected_active(T) == pytest.approx(expected, abs=0.05)
+
+
+def test_prefill_path_matches_library_choice():
+    """bench labels a configuration MFMA-bound exactly where the library runs the 128-row
+    prefill GEMM (16-row tiles up to 8 pairs per expert, 32-row up to 16, then 128-row)."""
+    for shape in (bench.S30B, bench.S235B):
+        for T in (1, 64, 128, 256, 257, 1024, 4096):
+            S = T * bench.K_TOP
+            bm = 16 if S <= 8 * shape.E else 32 if S <= 16 * shape.E else 128
+            assert shape.prefill_path(T) == (bm == 128), (shape.name, T)
+
+
+def test_weight_rotation_defeats_the_last_level_cache():
+    """With bench's 16 copies of the 30B experts, a copy is revisited only after at least twice
+    the 256 MB last-level cache of other weights, at every batch size."""
+    layer = bench.Layer.__new__(bench.Layer)
+    layer.shape = bench.S30B
+    layer.copies = [None] * 16
+    for T in (1, 8, 64, 256, 4096):
+        n = layer.n_rot(T)
+        per_step = layer.shape.layer_bytes(layer.shape.expected_active(T), T)
+        assert 2 <= n <= 16 and (n - 1) * per_step >= bench.LLC_BYTES, (T, n)
