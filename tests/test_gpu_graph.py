@@ -19,7 +19,7 @@ from tests.helpers import gpu_weights, to_bf16
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 300])
+@pytest.mark.parametrize("T", [1, 8, 64, 200, 300])  # 16-, 16-, 16-, 32- and 128-row tiles
 def test_block_graph_replays_match_eager(pkg, dev, T):
     E, H, I, k = 128, 2048, 768, 8
     q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=2)
