@@ -33,6 +33,8 @@
 namespace {
 
 typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHD = 128;        // head dim
 constexpr int kPage = 16;       // tokens per page
@@ -162,17 +164,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   auto page_of = [&](int p) __attribute__((always_inline)) {
     return (long)__builtin_amdgcn_readlane(my_page, (p - p_begin - wave) / kAttnWaves);
   };
+  // K and V are read once per step: non-temporal loads (the nt bit) keep the stream from
+  // displacing what the caches hold for reuse (5.24 -> 5.40 TB/s at the config-5 batch)
   auto load_k = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
     const uint16_t* kb = a.k_cache + (pg * a.Hkv + g) * kv_head_stride;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) kr[kk] = *(const uint4*)(kb + lr * kHD + 32 * kk + 8 * lg);
+    for (int kk = 0; kk < 4; ++kk)
+      kr[kk] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4*)(kb + lr * kHD + 32 * kk + 8 * lg)));
   };
   auto load_v = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
     const uint16_t* vb = a.v_cache + (pg * a.Hkv + g) * kv_head_stride;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) vr[n] = *(const uint2*)(vb + (16 * n + lr) * kPage + 4 * lg);
+    for (int n = 0; n < 8; ++n)
+      vr[n] = __builtin_bit_cast(uint2, __builtin_nontemporal_load((const u32x2*)(vb + (16 * n + lr) * kPage + 4 * lg)));
   };
 
   int p = p_begin + wave;
