@@ -33,8 +33,15 @@
 namespace {
 
 typedef short v4s __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Buffer descriptor of one (page, kv head) block of K or V (4 KB; offsets past it read 0).
+// Word 3 selects the 32-bit data format: untyped buffer loads on gfx9 read zeros when the
+// format field is 0.
+constexpr int kKvBlockBytes = 16 * 128 * 2;
+constexpr int kCachePolicyNT = 2;  // the instruction's cache-policy field: nt (streaming)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const uint16_t* block) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)block, (short)0, kKvBlockBytes, 0x00020000);
+}
 
 constexpr int kHD = 128;        // head dim
 constexpr int kPage = 16;       // tokens per page
@@ -165,20 +172,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     return (long)__builtin_amdgcn_readlane(my_page, (p - p_begin - wave) / kAttnWaves);
   };
   // K and V are read once per step: non-temporal loads (the nt bit) keep the stream from
-  // displacing what the caches hold for reuse (5.24 -> 5.40 TB/s at the config-5 batch)
+  // displacing what the caches hold for reuse (5.24 -> 5.40 TB/s at the config-5 batch), issued
+  // as buffer loads on a per-(page, kv head) descriptor (SGPR base, 32-bit lane offsets within
+  // the 4 KB block: 215.9 -> 212.4 us against global loads)
   auto load_k = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const uint16_t* kb = a.k_cache + (pg * a.Hkv + g) * kv_head_stride;
+    const __amdgpu_buffer_rsrc_t rk = kv_rsrc(a.k_cache + (pg * a.Hkv + g) * kv_head_stride);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      kr[kk] = __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4*)(kb + lr * kHD + 32 * kk + 8 * lg)));
+      kr[kk] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, (lr * kHD + 32 * kk + 8 * lg) * 2, 0,
+                                                                                 kCachePolicyNT));
   };
   auto load_v = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const uint16_t* vb = a.v_cache + (pg * a.Hkv + g) * kv_head_stride;
+    const __amdgpu_buffer_rsrc_t rv = kv_rsrc(a.v_cache + (pg * a.Hkv + g) * kv_head_stride);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
-      vr[n] = __builtin_bit_cast(uint2, __builtin_nontemporal_load((const u32x2*)(vb + (16 * n + lr) * kPage + 4 * lg)));
+      vr[n] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, ((16 * n + lr) * kPage + 4 * lg) * 2, 0,
+                                                                                kCachePolicyNT));
   };
 
   int p = p_begin + wave;
