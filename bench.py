@@ -266,37 +266,51 @@ def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
     return entry
 
 
-def cpu_baseline(torch, layer, router, x, budget_s=20.0):
-    """The CPU oracle (dequantise-then-fp32-matmul restatement of the reference path), timed
-    on this host on the headline workload; median over as many steps as fit the budget."""
-    import numpy as np
-
-    from oracle import moe_oracle as orc
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    q13, s13, q2, s2 = layer.copies[0]
-    q13n, q2n = q13.view(torch.uint8).cpu().numpy(), q2.view(torch.uint8).cpu().numpy()
-    s13n, s2n = s13.cpu().numpy(), s2.cpu().numpy()
-    xn, wrn = x.float().cpu().numpy(), router.float().cpu().numpy()
-    T = xn.shape[0]
-    times = []
-    t_all = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        lg, ids, w = orc.route(xn, wrn, K_TOP)
-        orc.experts_fp8(xn, ids, w, q13n, s13n, q2n, s2n, acc=np.float32)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all > budget_s or len(times) >= 10:
-            break
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(torch, layer, router, x, warmup=3, runs=10):
+    """The reference's PyTorch CPU path (oracle/torch_ref.py: transformers' router and
+    grouped_mm experts forward restated op for op, FP8 weights dequantised once to fp32, dynamic
+    activation quantisation), timed on this host's cores on the headline workload: `warmup`
+    untimed block forwards, then the median of `runs`."""
+    from oracle import torch_ref
+
+    # the box grants this job a CPU share (OMP_NUM_THREADS) that can be far below os.cpu_count()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        q13, s13, q2, s2 = (t.cpu() for t in layer.copies[0])
+        w13f = torch_ref.dequantize_weight(q13, s13)
+        w2f = torch_ref.dequantize_weight(q2, s2)
+        xc, wrc = x.cpu(), router.cpu()
+        T = xc.shape[0]
+        times = []
+        with torch.no_grad():
+            for i in range(warmup + runs):
+                t0 = time.perf_counter()
+                torch_ref.block_fp8_dequant(xc, wrc, K_TOP, w13f, w2f)
+                if i >= warmup:
+                    times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev_threads)
     med = sorted(times)[len(times) // 2]
     return {"value": round(T / med, 2), "unit": "tokens/s", "us_per_layer": round(med * 1e6, 1),
-            "cores": threads, "kind": "port",
-            "sample": f"{len(times)} block forwards of the {T}-token batch (numpy oracle: router, "
-                      f"per-expert dequantise then fp32 matmul), median"}
+            "cores": threads, "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+            "impl": "torch CPU (the reference's DEVICE=cpu path: transformers router + grouped_mm experts "
+                    "forward restated in torch, oracle/torch_ref.py)",
+            "sample": f"the {T}-token headline batch: {warmup} warm-up block forwards, median of {runs} "
+                      f"(router, sort, histc, cumsum, fp32 grouped_mm on FP8 weights dequantised once, "
+                      f"dynamic activation quantisation, combine), torch.set_num_threads({threads})"}
 
 
 def decode_step_entry(pkg, torch, dev, steps=10, n_layers=48, batch=128, seed=0):

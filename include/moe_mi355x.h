@@ -127,6 +127,16 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
                          void* weights, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Which of the block path's batch-size-dependent launch choices can change its output bits
+ * (the router GEMM's K chunks and kernel, the expert GEMMs' tile height): two batch sizes with
+ * the same key compute every token's row the same way.  0 for unsupported shapes.  A query
+ * (host only): a caller that pads batches up to a captured size (a HIP graph per batch bucket)
+ * splits its buckets where the key changes, so that a padded batch reproduces the unpadded one
+ * bit for bit.  No counterpart in the reference (its eager forward has no buckets).
+ */
+long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k);
+
+/*
  * Paged GQA decode attention, one new token per sequence (the attention of a decode step of
  * Qwen3MoeAttention.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:151-191, with
  * eager_attention_forward :96-119): for query head h of sequence b, over the keys
@@ -137,10 +147,13 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
  *   k_cache      bf16 [pages, Hkv, 16, 128] (token rows)
  *   v_cache      bf16 [pages, Hkv, 128, 16] (transposed: dim rows)
  *   block_tables int32 [B, max_pages]       page of each 16-token block of a sequence (device
- *                                           data, not checked: the entries a context covers must
- *                                           be page indices of the pools)
+ *                                           data); an entry outside [0, num_pages) (a -1 pad, a
+ *                                           stale id) is an empty page: it is never read and its
+ *                                           keys are left out of the softmax
  *   context_lens int32 [B]                  >= 1, <= 16 * max_pages (device data: a larger value
- *                                           is clamped to the table, 0 gives a zero output)
+ *                                           is clamped to the table; 0, or a context whose pages
+ *                                           are all empty, gives a zero output)
+ *   num_pages                               pages in each of k_cache and v_cache
  * The KV layout is this library's; the reference keeps a contiguous per-layer cache.
  * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16; q, k_cache,
  * v_cache and out 16-byte aligned.
@@ -148,19 +161,19 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
 size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages);
 int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,
                                  const int32_t* block_tables, const int32_t* context_lens, int B, int Hq,
-                                 int Hkv, int head_dim, int page_size, int max_pages, float scale, void* out,
-                                 void* workspace, size_t workspace_bytes, void* stream);
+                                 int Hkv, int head_dim, int page_size, int max_pages, int num_pages, float scale,
+                                 void* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * KV-cache append of one token per sequence at position positions[b] (the cache update of
  * Qwen3MoeAttention.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:170-171, in the paged
  * layout above).  k, v: bf16 [B, Hkv, 128] (k after k_norm and rotary embedding).
  * positions[b] in [0, 16 * max_pages), its page allocated in block_tables; a position outside
- * the table writes nothing.
+ * the table, or a table entry outside [0, num_pages), writes nothing.
  */
 int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
                          const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
-                         int head_dim, int page_size, int max_pages, void* stream);
+                         int head_dim, int page_size, int max_pages, int num_pages, void* stream);
 
 /*
  * RMSNorm over the last axis: out = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps)))), fp32
@@ -181,12 +194,13 @@ int moe_mi355x_rms_norm(const void* x, const void* weight, int rows, int cols, f
  *   q_norm_w, k_norm_w bf16 [128]          inv_freq fp32 [64]      positions int32 [B]
  *   q_out    bf16 [B, Hq, 128]
  * positions[b] in [0, 16 * max_pages), its page allocated in block_tables; for a position
- * outside the table q is written and the cache is not.
+ * outside the table, or a table entry outside [0, num_pages), q is written and the cache is not.
  */
 int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                                    const float* inv_freq, const int32_t* positions, int B, int Hq, int Hkv,
                                    int head_dim, float eps, void* q_out, void* k_cache, void* v_cache,
-                                   const int32_t* block_tables, int page_size, int max_pages, void* stream);
+                                   const int32_t* block_tables, int page_size, int max_pages, int num_pages,
+                                   void* stream);
 
 /*
  * MoE sublayer of a decoder layer: out = h' + moe_block(rms_norm(h', ln_weight)) with

@@ -36,13 +36,15 @@ SIGNATURES = {
     "moe_mi355x_block_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_block_fp8": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_size, _vp]),
+    "moe_mi355x_block_numerics_key": (ctypes.c_longlong, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_paged_attn_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_paged_attn_decode": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                              _c_int, ctypes.c_float, _vp, _vp, _c_size, _vp]),
-    "moe_mi355x_kv_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp]),
+                                              _c_int, _c_int, ctypes.c_float, _vp, _vp, _c_size, _vp]),
+    "moe_mi355x_kv_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _vp]),
     "moe_mi355x_rms_norm": (_c_int, [_vp, _vp, _c_int, _c_int, ctypes.c_float, _vp, _vp]),
     "moe_mi355x_qk_norm_rope_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
-                                                ctypes.c_float, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp]),
+                                                ctypes.c_float, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "moe_mi355x_moe_sublayer_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_moe_sublayer_fp8": (_c_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _c_int, _c_int,
                                              _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),

@@ -39,8 +39,8 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 // format field is 0.
 constexpr int kKvBlockBytes = 16 * 128 * 2;
 constexpr int kCachePolicyNT = 2;  // the instruction's cache-policy field: nt (streaming)
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const uint16_t* block) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)block, (short)0, kKvBlockBytes, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const uint16_t* block, bool live) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)block, (short)0, live ? kKvBlockBytes : 0, 0x00020000);
 }
 
 constexpr int kHD = 128;        // head dim
@@ -82,6 +82,7 @@ struct AttnArgs {
   float* part_o;               // [B, Hkv, max_splits, G, 128] unnormalised outputs
   float* part_ml;              // [B, Hkv, max_splits, G, 2] (running max, sum)
   int B, Hq, Hkv, max_pages, max_splits, pps;
+  int num_pages;               // pages in each pool: table entries outside [0, num_pages) are empty
   float scale;
 };
 
@@ -171,13 +172,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   auto page_of = [&](int p) __attribute__((always_inline)) {
     return (long)__builtin_amdgcn_readlane(my_page, (p - p_begin - wave) / kAttnWaves);
   };
+  // a table entry outside the pools (a -1 pad, a stale id) is an empty page: its descriptor
+  // covers 0 bytes, so its loads read zeros and touch no memory, and its keys are masked
+  auto page_ok = [&](long pg) __attribute__((always_inline)) { return pg >= 0 && pg < a.num_pages; };
   // K and V are read once per step: non-temporal loads (the nt bit) keep the stream from
   // displacing what the caches hold for reuse (5.24 -> 5.40 TB/s at the config-5 batch), issued
   // as buffer loads on a per-(page, kv head) descriptor (SGPR base, 32-bit lane offsets within
   // the 4 KB block: 215.9 -> 212.4 us against global loads)
   auto load_k = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const __amdgpu_buffer_rsrc_t rk = kv_rsrc(a.k_cache + (pg * a.Hkv + g) * kv_head_stride);
+    const bool ok = page_ok(pg);
+    const __amdgpu_buffer_rsrc_t rk = kv_rsrc(a.k_cache + ((ok ? pg : 0) * a.Hkv + g) * kv_head_stride, ok);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       kr[kk] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, (lr * kHD + 32 * kk + 8 * lg) * 2, 0,
@@ -185,7 +190,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   };
   auto load_v = [&](int p) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const __amdgpu_buffer_rsrc_t rv = kv_rsrc(a.v_cache + (pg * a.Hkv + g) * kv_head_stride);
+    const bool ok = page_ok(pg);
+    const __amdgpu_buffer_rsrc_t rv = kv_rsrc(a.v_cache + ((ok ? pg : 0) * a.Hkv + g) * kv_head_stride, ok);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
       vr[n] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, ((16 * n + lr) * kPage + 4 * lg) * 2, 0,
@@ -206,21 +212,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kr[kk]), qop[kk], s, 0, 0, 0);
     if (more) load_k(p + kAttnWaves);
     const int key0 = p * kPage + 4 * lg;
+    const int key_end = page_ok(page_of(p)) ? ctx : 0;  // an empty page has no live keys
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // the reference's rounding: bf16 matmul output, then a bf16 multiply by the scale
       const float x = bf16_round(bf16_round(s[i]) * a.scale);
-      sv[i] = key0 + i < ctx ? x : -INFINITY;
+      sv[i] = key0 + i < key_end ? x : -INFINITY;
     }
     float pm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     pm = rows_max(pm);
-    const float m_new = fmaxf(m_run, pm);  // finite: every page has at least one live key
-    const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * 1.4426950408889634f);  // 0 on the first page
+    const float m_new = fmaxf(m_run, pm);  // -inf only while every page so far was empty
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float corr = __builtin_amdgcn_exp2f((m_run - m_ref) * 1.4426950408889634f);  // 0 on the first page
     float pv[4], ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pv[i] = __builtin_amdgcn_exp2f((sv[i] - m_new) * 1.4426950408889634f);
+      pv[i] = __builtin_amdgcn_exp2f((sv[i] - m_ref) * 1.4426950408889634f);
       ps += pv[i];
     }
     ps = rows_sum(ps);
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     // keys past the end of the sequence (last page) have P = 0; their V slots may hold
     // anything (the pool is not cleared), so they are zeroed rather than multiplied by 0:
     // keys 4 lg + j with j < live_keys are valid (j = 0, 1 in v.x, j = 2, 3 in v.y)
-    const int live_keys = ctx - key0;
+    const int live_keys = key_end - key0;
     const uint32_t mask_x = live_keys >= 2 ? 0xffffffffu : (live_keys == 1 ? 0xffffu : 0u);
     const uint32_t mask_y = live_keys >= 4 ? 0xffffffffu : (live_keys == 3 ? 0xffffu : 0u);
 #pragma unroll
@@ -335,13 +343,18 @@ __global__ __launch_bounds__(256) void paged_attn_merge_kernel(AttnArgs a, uint1
 #pragma unroll
       for (int u = 0; u < kMergeUnroll; ++u) {
         if (s0 + u >= ns) break;
-        const float w = __builtin_amdgcn_exp2f((ml[u].x - M) * 1.4426950408889634f);
+        // a split of empty pages only has m = -inf and adds nothing
+        const float w = ml[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((ml[u].x - M) * 1.4426950408889634f);
         L += ml[u].y * w;
         acc[0] += ov[u].x * w;
         acc[1] += ov[u].y * w;
         acc[2] += ov[u].z * w;
         acc[3] += ov[u].w * w;
       }
+    }
+    if (L == 0.f) {  // every page of the context empty: as an empty context
+      *(uint2*)dst = make_uint2(0u, 0u);
+      continue;
     }
     *(uint2*)dst = make_uint2((uint32_t)f32_to_bf16(acc[0] / L) | ((uint32_t)f32_to_bf16(acc[1] / L) << 16),
                               (uint32_t)f32_to_bf16(acc[2] / L) | ((uint32_t)f32_to_bf16(acc[3] / L) << 16));
@@ -353,11 +366,13 @@ __global__ __launch_bounds__(256) void paged_attn_merge_kernel(AttnArgs a, uint1
 __global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                         uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
                                                         const int32_t* __restrict__ block_tables,
-                                                        const int32_t* __restrict__ positions, int Hkv, int max_pages) {
+                                                        const int32_t* __restrict__ positions, int Hkv, int max_pages,
+                                                        int num_pages) {
   const int b = blockIdx.x;
   const int pos = positions[b];
   if (pos < 0 || pos >= kPage * max_pages) return;  // outside the block table: nothing to write
   const long pg = block_tables[(long)b * max_pages + pos / kPage];
+  if (pg < 0 || pg >= num_pages) return;  // a table entry outside the pools: nothing to write
   const int slot = pos % kPage;
   for (int i = threadIdx.x; i < Hkv * kHD; i += blockDim.x) {
     const int g = i / kHD, d = i % kHD;
@@ -376,9 +391,9 @@ int attn_pps(int B, int Hkv, int max_pages) {
   return pps;
 }
 
-bool attn_args_ok(int B, int Hq, int Hkv, int head_dim, int page_size, int max_pages) {
+bool attn_args_ok(int B, int Hq, int Hkv, int head_dim, int page_size, int max_pages, int num_pages) {
   return B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && head_dim == kHD &&
-         page_size == kPage && max_pages > 0;
+         page_size == kPage && max_pages > 0 && num_pages >= 0;
 }
 
 }  // namespace
@@ -393,9 +408,9 @@ extern "C" size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, 
 extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,
                                             const int32_t* block_tables, const int32_t* context_lens, int B,
                                             int Hq, int Hkv, int head_dim, int page_size, int max_pages,
-                                            float scale, void* out, void* workspace, size_t workspace_bytes,
-                                            void* stream) {
-  MOE_RETURN_IF(!attn_args_ok(B, Hq, Hkv, head_dim, page_size, max_pages), MOE_ERR_INVALID_ARG);
+                                            int num_pages, float scale, void* out, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  MOE_RETURN_IF(!attn_args_ok(B, Hq, Hkv, head_dim, page_size, max_pages, num_pages), MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!q || !k_cache || !v_cache || !block_tables || !context_lens || !out, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!moe_aligned16(q) || !moe_aligned16(k_cache) || !moe_aligned16(v_cache) || !moe_aligned16(out),
                 MOE_ERR_ALIGNMENT);
@@ -408,7 +423,7 @@ extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, 
   float* part_o = c.take<float>((size_t)parts * kHD);
   float* part_ml = c.take<float>((size_t)parts * 2);
   AttnArgs a{(const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables, context_lens,
-             part_o, part_ml, B, Hq, Hkv, max_pages, ms, pps, scale};
+             part_o, part_ml, B, Hq, Hkv, max_pages, ms, pps, num_pages, scale};
   hipStream_t s = (hipStream_t)stream;
   // an upper bound of the (b, g, split) items; the kernel maps workgroups to the live ones
   hipLaunchKernelGGL(paged_attn_decode_kernel, dim3((unsigned)((long)B * Hkv * ms)), dim3(256), 0, s, a);
@@ -420,12 +435,13 @@ extern "C" int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, 
 
 extern "C" int moe_mi355x_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
                                     const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
-                                    int head_dim, int page_size, int max_pages, void* stream) {
-  MOE_RETURN_IF(B <= 0 || Hkv <= 0 || head_dim != kHD || page_size != kPage || max_pages <= 0, MOE_ERR_INVALID_ARG);
+                                    int head_dim, int page_size, int max_pages, int num_pages, void* stream) {
+  MOE_RETURN_IF(B <= 0 || Hkv <= 0 || head_dim != kHD || page_size != kPage || max_pages <= 0 || num_pages < 0,
+                MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!k || !v || !k_cache || !v_cache || !block_tables || !positions, MOE_ERR_INVALID_ARG);
   hipLaunchKernelGGL(kv_append_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)k,
                      (const uint16_t*)v, (uint16_t*)k_cache, (uint16_t*)v_cache, block_tables, positions, Hkv,
-                     max_pages);
+                     max_pages, num_pages);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
     const float* __restrict__ inv_freq, const int32_t* __restrict__ positions, int B, int Hq, int Hkv, float eps,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ block_tables, int max_pages) {
+    const int32_t* __restrict__ block_tables, int max_pages, int num_pages) {
   // x * cos + rotate_half(x) * sin: both products are rounded to bf16 before the sum (the
   // reference's separate bf16 ops), so no multiply-add contraction here
 #pragma clang fp contract(off)
@@ -100,10 +100,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   const uint16_t* src = qkv + ((long)b * nh + h) * kHD;
   float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
   const int pos = positions[b];
-  // a position outside the block table has no page: q is still written, the cache is not
+  // a position outside the block table, or a table entry outside the pools (a -1 pad, a stale
+  // id), has no page: q is still written, the cache is not
   const bool in_table = pos >= 0 && pos < kPage * max_pages;
-  if (!in_table && h >= Hq) return;
-  const long page = in_table ? block_tables[(long)b * max_pages + pos / kPage] : 0;
+  const long page = in_table ? block_tables[(long)b * max_pages + pos / kPage] : -1;
+  if ((page < 0 || page >= num_pages) && h >= Hq) return;
   const int slot = pos % kPage;
   if (h >= Hq + Hkv) {  // v head: transposed page rows
     const int g = h - Hq - Hkv;
@@ -166,8 +167,9 @@ extern "C" int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_nor
                                               const float* inv_freq, const int32_t* positions, int B, int Hq,
                                               int Hkv, int head_dim, float eps, void* q_out, void* k_cache,
                                               void* v_cache, const int32_t* block_tables, int page_size,
-                                              int max_pages, void* stream) {
-  MOE_RETURN_IF(B < 0 || Hq <= 0 || Hkv <= 0 || head_dim != kHD || page_size != kPage || max_pages <= 0,
+                                              int max_pages, int num_pages, void* stream) {
+  MOE_RETURN_IF(B < 0 || Hq <= 0 || Hkv <= 0 || head_dim != kHD || page_size != kPage || max_pages <= 0 ||
+                    num_pages < 0,
                 MOE_ERR_INVALID_ARG);
   if (B == 0) return MOE_OK;
   MOE_RETURN_IF(!qkv || !q_norm_w || !k_norm_w || !inv_freq || !positions || !q_out || !k_cache || !v_cache ||
@@ -177,7 +179,7 @@ extern "C" int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_nor
   hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, inv_freq, positions,
                      B, Hq, Hkv, eps, (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, block_tables,
-                     max_pages);
+                     max_pages, num_pages);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }

@@ -280,6 +280,13 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
 }
 }  // namespace
 
+int moe_route_numerics_key(int T, int H, int E);
+
+extern "C" long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k) {
+  if (!experts_args_ok(T, H, I, E, k, 4) || T == 0) return 0;
+  return ((long long)moe_route_numerics_key(T, H, E) << 16) | moe_gemm_block_m(T * k, E, H, I);
+}
+
 extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,
                                     int renorm, const void* w13, const float* s13, const void* w2,
                                     const float* s2, void* out, void* logits, void* ids, int id_bytes,

@@ -427,6 +427,16 @@ extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E) {
   return moe_align_up((size_t)ks * T * E * sizeof(float), 256);
 }
 
+// What of the block path's routing depends on the batch size and can change the bits of the
+// logits: the GEMM kernel (tiled or not) and the K chunks whose fp32 partials are summed.
+int moe_route_numerics_key(int T, int H, int E) {
+  if (T <= 0 || H <= 0 || E <= 0) return 0;
+  const int ks = route_ksplit(T, H, E);
+  const bool tiled = route_tiled(T, H);
+  const int kchunk = route_kchunk(H, ks, true);
+  return (tiled ? 1 << 16 : 0) | kchunk;
+}
+
 // Whether moe_launch_route can run the top-k and the expert sort as one workgroup.
 bool moe_route_can_fuse_align(int T, int E, int k) {
   // one workgroup routes every token, so the whole top-k runs on one CU: a win over the

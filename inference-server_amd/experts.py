@@ -14,6 +14,10 @@ torch_backend.py:38-40); for a Qwen3-MoE checkpoint each decoder layer calls
 * ``MI355XSparseMoeBlock`` replaces a whole ``Qwen3MoeSparseMoeBlock``
   (modeling_qwen3_moe.py:270-281) with ``forward(hidden_states[B,S,H]) -> [B,S,H]``;
   ``swap_moe_blocks(model)`` does it for every layer after ``load_model``.
+
+Both run their kernels through the registered operators ``torch.ops.moe_mi355x.*``
+(``torch_ops``), so a model compiled with ``torch.compile`` (the reference's ``COMPILE_MODEL``,
+torch_backend.py:44-47) traces through the MoE blocks without a graph break.
 """
 
 from __future__ import annotations
@@ -21,7 +25,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import kernels
+from . import _lib, kernels, torch_ops  # noqa: F401  (torch_ops registers torch.ops.moe_mi355x)
 
 IMPLEMENTATION_KEY = "mi355x"
 
@@ -53,8 +57,8 @@ def mi355x_fp8_experts_forward(self: nn.Module, hidden_states: torch.Tensor, top
     out_dtype = hidden_states.dtype
     x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
     w = top_k_weights if top_k_weights.dtype == torch.bfloat16 else top_k_weights.to(torch.bfloat16)
-    out = kernels.experts_fp8(x.contiguous(), top_k_index.contiguous(), w.contiguous(), self.gate_up_proj,
-                              self.gate_up_proj_scale_inv, self.down_proj, self.down_proj_scale_inv)
+    out = torch.ops.moe_mi355x.moe_fp8(x.contiguous(), top_k_index.contiguous(), w.contiguous(), self.gate_up_proj,
+                                       self.gate_up_proj_scale_inv, self.down_proj, self.down_proj_scale_inv)
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
 
@@ -123,7 +127,9 @@ class MI355XTopKRouter(nn.Module):
 
     def forward(self, hidden_states):
         x = hidden_states.reshape(-1, self.hidden_dim)
-        return kernels.route(x.contiguous(), self.weight, self.top_k, self.norm_topk_prob)
+        ids, scores, logits = torch.ops.moe_mi355x.route(x.contiguous(), self.weight, self.top_k,
+                                                          bool(self.norm_topk_prob))
+        return logits, scores, ids.to(torch.int64)  # the reference's int64 indices
 
 
 class MI355XSparseMoeBlock(nn.Module):
@@ -136,10 +142,22 @@ class MI355XSparseMoeBlock(nn.Module):
         self.experts = MI355XFp8Experts(num_experts, hidden_dim, intermediate_dim, device=device)
 
     @classmethod
-    def from_hf_block(cls, block: nn.Module, norm_topk_prob: bool | None = None) -> "MI355XSparseMoeBlock":
-        """Build from a ``Qwen3MoeSparseMoeBlock`` with bf16 experts (quantised here, 128x128 blocks)
-        or from one whose experts already carry ``FP8Experts`` parameters."""
+    def from_hf_block(cls, block: nn.Module, norm_topk_prob: bool | None = None,
+                      quantize_fp8: bool = False) -> "MI355XSparseMoeBlock":
+        """Build from a ``Qwen3MoeSparseMoeBlock`` whose experts carry ``FP8Experts`` parameters,
+        or, with ``quantize_fp8=True``, from one with bf16 / fp32 experts, quantised here per
+        128x128 block (``Fp8Quantize``, finegrained_fp8.py:903-941).
+
+        The reference loads checkpoints in bf16 (torch_backend.py:38-40) and runs bf16 experts;
+        FP8 requantisation changes the block's numerics (dynamic activation quantisation, FP8
+        weights), so it is never done silently: bf16 experts without ``quantize_fp8=True`` raise
+        ``ValueError``."""
         gate, experts = block.gate, block.experts
+        if experts.gate_up_proj.dtype != torch.float8_e4m3fn and not quantize_fp8:
+            raise ValueError(
+                f"the experts hold {experts.gate_up_proj.dtype} weights; this block computes in FP8 "
+                "(e4m3, 128x128 block scales, dynamic per-token activation quantisation), which changes the "
+                "model's numerics against its bf16 experts: pass quantize_fp8=True to requantise them")
         E, H = gate.weight.shape
         renorm = gate.norm_topk_prob if norm_topk_prob is None else norm_topk_prob
         dev = gate.weight.device
@@ -157,23 +175,47 @@ class MI355XSparseMoeBlock(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         e = self.experts
-        return kernels.moe_block_fp8(hidden_states.contiguous(), self.gate.weight, self.gate.top_k, e.gate_up_proj,
-                                     e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv,
-                                     norm_topk_prob=self.gate.norm_topk_prob)
+        return torch.ops.moe_mi355x.moe_block_fp8(hidden_states.contiguous(), self.gate.weight, self.gate.top_k,
+                                                  bool(self.gate.norm_topk_prob), e.gate_up_proj,
+                                                  e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv)
 
 
-def swap_moe_blocks(model: nn.Module) -> int:
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256)
+
+
+def swap_moe_blocks(model: nn.Module, quantize_fp8: bool = False, graphed: bool = False,
+                    buckets=DEFAULT_BUCKETS) -> int:
     """Replace every Qwen3-MoE sparse block of ``model`` by ``MI355XSparseMoeBlock``; returns the count.
 
     Intended right after the reference's ``TorchBackend.load_model`` (torch_backend.py:33-53).
+    ``quantize_fp8``: requantise bf16 experts to FP8 (see ``MI355XSparseMoeBlock.from_hf_block``;
+    without it bf16 experts raise).  ``graphed``: wrap each block in ``MI355XGraphedMoeBlock``, so
+    that decode batches up to the largest bucket replay a captured HIP graph (the reference's
+    decode loop calls the model once per scheduler step, scheduler.py:396-398).
     """
     targets = [(name, mod) for name, mod in model.named_modules()
                if type(mod).__name__ == "Qwen3MoeSparseMoeBlock"]
     for name, mod in targets:
         parent_name, _, child = name.rpartition(".")
         parent = model.get_submodule(parent_name) if parent_name else model
-        setattr(parent, child, MI355XSparseMoeBlock.from_hf_block(mod))
+        new = MI355XSparseMoeBlock.from_hf_block(mod, quantize_fp8=quantize_fp8)
+        setattr(parent, child, MI355XGraphedMoeBlock(new, buckets) if graphed else new)
     return len(targets)
+
+
+def numerics_buckets(buckets, hidden: int, intermediate: int, num_experts: int, top_k: int) -> tuple:
+    """``buckets`` plus an edge at every batch size where the block's numerics key changes
+    (``moe_mi355x_block_numerics_key``: router K chunks and kernel, expert tile height), so that
+    every batch size in (previous bucket, bucket] computes its rows exactly as the bucket does."""
+    buckets = sorted(set(int(b) for b in buckets if int(b) >= 1))
+    if not buckets:
+        return ()
+    lib = _lib.load()
+    keys = [lib.moe_mi355x_block_numerics_key(t, hidden, intermediate, num_experts, top_k)
+            for t in range(1, buckets[-1] + 1)]
+    edges = set(buckets)
+    edges.update(t for t in range(1, buckets[-1]) if keys[t - 1] != keys[t])
+    return tuple(sorted(edges))
 
 
 class MI355XGraphedMoeBlock(nn.Module):
@@ -184,18 +226,32 @@ class MI355XGraphedMoeBlock(nn.Module):
     not the weight stream, sets the MoE layer's time.  This wrapper captures the block's launches
     once per bucket size (the smallest bucket >= the batch; batches are zero-padded up to it, and
     the padded rows' outputs are dropped) and replays the graph afterwards.  Batches above the
-    largest bucket run eagerly.  Inputs are copied into the graph's static buffer, so the caller's
+    largest bucket run eagerly.  The buckets are split wherever the library's batch-size-dependent
+    launch choices that touch the output bits change (``numerics_buckets``), and every row of a
+    batch is computed independently of the other rows, so a padded replay returns exactly the
+    eager block's output; the padding rows (zeros) only add their routed experts' weight stream.  Inputs are copied into the graph's static buffer, so the caller's
     tensors may live anywhere.  The output (bf16 inputs) is a view of the graph's static output
     buffer, valid until this module's next call: clone it to keep it longer (the decoder layer
     consumes it at once in its residual add, modeling_qwen3_moe.py:347).  Graphs are captured on
     first use of a bucket; ``capture()`` captures them up front.
     """
 
-    def __init__(self, block: MI355XSparseMoeBlock, buckets=(1, 2, 4, 8, 16, 32, 64, 128, 256)):
+    def __init__(self, block: MI355XSparseMoeBlock, buckets=DEFAULT_BUCKETS):
         super().__init__()
         self.block = block
-        self.buckets = tuple(sorted(set(int(b) for b in buckets)))
+        self.requested_buckets = tuple(sorted(set(int(b) for b in buckets)))
+        self.buckets = numerics_buckets(buckets, block.gate.hidden_dim, block.experts.intermediate_dim,
+                                        block.gate.num_experts, block.gate.top_k)
         self._graphs: dict[int, tuple] = {}
+
+    # the wrapped block's modules, so that code written for MI355XSparseMoeBlock finds them
+    @property
+    def gate(self) -> MI355XTopKRouter:
+        return self.block.gate
+
+    @property
+    def experts(self) -> MI355XFp8Experts:
+        return self.block.experts
 
     def _bucket(self, t: int) -> int | None:
         for b in self.buckets:

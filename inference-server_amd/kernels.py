@@ -308,7 +308,7 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     ws = _ws(lib.moe_mi355x_paged_attn_workspace_bytes(B, Hq, Hkv, max_pages), q.device)
     _lib.check(lib.moe_mi355x_paged_attn_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                                 block_tables.data_ptr(), context_lens.data_ptr(), B, Hq, Hkv,
-                                                HEAD_DIM, PAGE_SIZE, max_pages, float(scale), out.data_ptr(),
+                                                HEAD_DIM, PAGE_SIZE, max_pages, P, float(scale), out.data_ptr(),
                                                 ws.data_ptr(), ws.numel(), _stream(q)), "paged_attn_decode")
     return out
 
@@ -331,7 +331,8 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
         raise ValueError("block_tables and positions need one row per sequence")
     _lib.check(_lib.load().moe_mi355x_kv_append(k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                                 block_tables.data_ptr(), positions.data_ptr(), B, Hkv, HEAD_DIM,
-                                                PAGE_SIZE, block_tables.shape[1], _stream(k)), "kv_append")
+                                                PAGE_SIZE, block_tables.shape[1], k_cache.shape[0], _stream(k)),
+               "kv_append")
 
 
 # ---------------------------------------------------------------------------
@@ -378,7 +379,8 @@ def qk_norm_rope_append(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_w
     _lib.check(_lib.load().moe_mi355x_qk_norm_rope_append(
         qkv.data_ptr(), q_norm_weight.data_ptr(), k_norm_weight.data_ptr(), inv_freq.data_ptr(), positions.data_ptr(),
         B, num_heads, num_kv_heads, HEAD_DIM, float(eps), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-        block_tables.data_ptr(), PAGE_SIZE, block_tables.shape[1], _stream(qkv)), "qk_norm_rope_append")
+        block_tables.data_ptr(), PAGE_SIZE, block_tables.shape[1], k_cache.shape[0], _stream(qkv)),
+        "qk_norm_rope_append")
     return q
 
 

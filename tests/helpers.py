@@ -28,7 +28,7 @@ def f8_codes(t):
 
 
 def np_f32(t):
-    return t.float().cpu().numpy()
+    return t.detach().float().cpu().numpy()
 
 
 def bf16_ulp_diff(a, b):

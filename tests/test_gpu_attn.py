@@ -180,3 +180,73 @@ def test_kv_append_skips_positions_outside_the_table(pkg, dev):
     expect_k[1, :, 4, :] = k[0]
     expect_v[1, :, :, 4] = v[0]
     assert np.array_equal(kcn, expect_k) and np.array_equal(vcn, expect_v)
+
+
+def test_paged_attention_skips_table_entries_outside_the_pools(pkg, dev):
+    """A block-table entry outside [0, pages) (a -1 pad, a stale id) inside a context is an empty
+    page: never read (its descriptor covers no bytes), its keys left out of the softmax.  The
+    output equals the attention over the valid pages' keys; a context whose every page is
+    invalid gives zeros, never NaN."""
+    rng = np.random.default_rng(14)
+    lens = [100, 700, 50]
+    Hq, Hkv = 32, 4
+    kc, vc, tables, seqs = build_cache(rng, lens, Hkv, poison=False)
+    n_pool = kc.shape[0]
+    tables = tables.copy()
+    # sequence 0 (7 pages): pages 1 and 5 invalid, so wave 1 of the split sees only empty pages
+    tables[0, 1] = -1
+    tables[0, 5] = n_pool + 3
+    # sequence 1 (44 pages, several splits): a run of invalid pages filling one whole split
+    tables[1, 8:24] = -7
+    tables[1, 30] = n_pool
+    # sequence 2: every page invalid
+    tables[2, :4] = -1
+    q = orc.round_bf16(rng.standard_normal((3, Hq, D)).astype(np.float32))
+    out = pkg.paged_attention_decode(to_bf16(q, dev), to_bf16(kc, dev), to_bf16(vc, dev),
+                                     torch.from_numpy(tables).to(dev), torch.tensor(lens, dtype=torch.int32, device=dev),
+                                     SCALE)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    refs = []
+    for b in range(2):
+        k, v = seqs[b]
+        keep = np.array([0 <= tables[b, t // PAGE] < n_pool for t in range(lens[b])])
+        refs.append(att.decode_attention(q[b], k[keep], v[keep], SCALE))
+    max_abs, mean_rel = errors(got[:2], np.stack(refs))
+    assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
+    assert np.array_equal(got[2], np.zeros_like(got[2]))
+
+
+def test_cache_writers_skip_table_entries_outside_the_pools(pkg, dev):
+    """kv_append and qk_norm_rope_append write nothing through a table entry outside the pools:
+    every pool byte is unchanged except the rows of the valid writes; q is still written."""
+    rng = np.random.default_rng(15)
+    B, Hq, Hkv, n_pages = 4, 8, 2, 6
+    kc0 = to_bf16(rng.standard_normal((n_pages, Hkv, PAGE, D)).astype(np.float32), dev)
+    vc0 = to_bf16(rng.standard_normal((n_pages, Hkv, D, PAGE)).astype(np.float32), dev)
+    tables = torch.tensor([[2, -1], [n_pages, 3], [5, 1], [-100, 4]], dtype=torch.int32, device=dev)
+    pos = torch.tensor([20, 3, 17, 0], dtype=torch.int32, device=dev)  # pages: -1, n_pages, 1, -100
+    k = to_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32), dev)
+    v = to_bf16(rng.standard_normal((B, Hkv, D)).astype(np.float32), dev)
+    kc, vc = kc0.clone(), vc0.clone()
+    pkg.kv_append(k, v, kc, vc, tables, pos)
+    ek, ev = kc0.clone(), vc0.clone()
+    ek[1, :, 1, :] = k[2]
+    ev[1, :, :, 1] = v[2]
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), ek.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), ev.view(torch.int16))
+
+    qkv = to_bf16(rng.standard_normal((B, (Hq + 2 * Hkv) * D)).astype(np.float32), dev)
+    nw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    inv = torch.from_numpy(att.default_inv_freq()).to(dev)
+    kc, vc = kc0.clone(), vc0.clone()
+    q = pkg.qk_norm_rope_append(qkv, nw, nw, inv, pos, Hq, Hkv, 1e-6, kc, vc, tables)
+    torch.cuda.synchronize()
+    changed_k = (kc.view(torch.int16) != kc0.view(torch.int16)).any(dim=(1, 3))  # [pages, slot]
+    changed_v = (vc.view(torch.int16) != vc0.view(torch.int16)).any(dim=(1, 2))
+    allowed = torch.zeros((n_pages, PAGE), dtype=torch.bool, device=dev)
+    allowed[1, 1] = True
+    assert not (changed_k & ~allowed).any() and not (changed_v & ~allowed).any()
+    assert changed_v[1, 1]
+    assert torch.isfinite(q.float()).all() and q.abs().sum() > 0

@@ -27,17 +27,28 @@ transformers = pytest.importorskip("transformers")
 PAGE = 16
 
 
-def _model(dev, n_layers=2, heads=4, kv_heads=2):
+def _model(dev, n_layers=2, heads=4, kv_heads=2, hidden=256, experts=16, top_k=4, moe_intermediate=128,
+           max_pos=512):
     from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeForCausalLM
 
-    cfg = Qwen3MoeConfig(vocab_size=128, hidden_size=256, intermediate_size=256, num_hidden_layers=n_layers,
-                         num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128, num_experts=16,
-                         num_experts_per_tok=4, moe_intermediate_size=128, norm_topk_prob=True,
-                         max_position_embeddings=512, rope_theta=1e6)
+    cfg = Qwen3MoeConfig(vocab_size=128, hidden_size=hidden, intermediate_size=256, num_hidden_layers=n_layers,
+                         num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=128, num_experts=experts,
+                         num_experts_per_tok=top_k, moe_intermediate_size=moe_intermediate, norm_topk_prob=True,
+                         max_position_embeddings=max_pos, rope_theta=1e6)
     cfg._attn_implementation = "eager"
     torch.manual_seed(0)
-    model = Qwen3MoeForCausalLM(cfg).to(torch.bfloat16).to(dev).eval()
+    with torch.device(dev):  # initialised on the GPU: the full-shape experts are GBs
+        model = Qwen3MoeForCausalLM(cfg).to(torch.bfloat16).eval()
+    # ``.to(bfloat16)`` also rounds the rotary embedding's inv_freq buffer to bf16, a phase error that
+    # grows with the position (a k difference of 1.0 at position 517); a checkpoint loaded with
+    # from_pretrained(dtype=bfloat16) (torch_backend.py:38-40) keeps it fp32, as computed by
+    # compute_default_rope_parameters (modeling_qwen3_moe.py:400-418)
+    rot = model.model.rotary_emb
+    exps = torch.arange(0, 128, 2, dtype=torch.float) / 128
+    inv_freq = (1.0 / (1e6 ** exps)).to(dev)
+    rot.register_buffer("inv_freq", inv_freq, persistent=False)
+    rot.register_buffer("original_inv_freq", inv_freq.clone(), persistent=False)
     with torch.no_grad():
         for layer in model.model.layers:
             layer.mlp.gate.weight.normal_(0, 0.02)
@@ -50,21 +61,20 @@ def _model(dev, n_layers=2, heads=4, kv_heads=2):
     return cfg, model
 
 
-@pytest.mark.parametrize("lens", [[23], [40, 17, 5]])
-def test_decode_step_matches_transformers(pkg, dev, lens):
+def _compare_decode_steps(pkg, dev, cfg, model, lens, n_steps=1, max_abs_scale=2e-2):
+    """Prefill (left padded) through transformers, copy its KV cache into the paged pools, then
+    run ``n_steps`` batched decode steps through both and compare the last layer's output."""
     from transformers import DynamicCache
 
     from inference_server_amd import decode as dec
 
-    cfg, model = _model(dev)
-    assert pkg.swap_moe_blocks(model) == cfg.num_hidden_layers
+    assert pkg.swap_moe_blocks(model, quantize_fp8=True) == cfg.num_hidden_layers
     B, S = len(lens), max(lens)
     ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev)
     # left padding, as the reference's batched decode does; the padded keys are masked out
     attn_mask = torch.zeros((B, S), dtype=torch.long, device=dev)
     for b, L in enumerate(lens):
         attn_mask[b, S - L:] = 1
-    nxt = torch.randint(0, cfg.vocab_size, (B, 1), device=dev)
     outs = {}
 
     def hook(mod, inp, out):
@@ -75,24 +85,19 @@ def test_decode_step_matches_transformers(pkg, dev, lens):
     with torch.no_grad():
         pos = (attn_mask.cumsum(-1) - 1).clamp(min=0)
         model(input_ids=ids, attention_mask=attn_mask, position_ids=pos, past_key_values=cache, use_cache=True)
-        full_mask = torch.cat([attn_mask, torch.ones((B, 1), dtype=torch.long, device=dev)], dim=1)
-        new_pos = torch.tensor(lens, device=dev).view(B, 1)
-        model(input_ids=nxt, attention_mask=full_mask, position_ids=new_pos, past_key_values=cache, use_cache=True)
-        ref = outs["last"].view(B, cfg.hidden_size)
-        emb = model.model.embed_tokens(nxt).view(B, cfg.hidden_size)
 
     dcfg = dec.DecoderConfig(hidden=cfg.hidden_size, heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads,
                              head_dim=128, experts=cfg.num_experts, top_k=cfg.num_experts_per_tok,
                              moe_intermediate=cfg.moe_intermediate_size, rms_eps=cfg.rms_norm_eps, rope_theta=1e6)
     layers = [dec.DecoderLayerWeights.from_hf_layer(l, dcfg) for l in model.model.layers]
-    max_pages = (S + 1 + PAGE - 1) // PAGE + 1
+    max_pages = (S + n_steps + PAGE - 1) // PAGE + 1
     n_pages = B * max_pages + 2
     kv = dec.PagedKVCache(cfg.num_hidden_layers, n_pages, cfg.num_key_value_heads, dev)
     # scattered page assignment
     perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(1)).to(torch.int32)
     tables = perm[: B * max_pages].view(B, max_pages).contiguous().to(dev)
     for i in range(cfg.num_hidden_layers):
-        k_all, v_all = cache.layers[i].keys, cache.layers[i].values  # [B, Hkv, S + 1, d], post-rotary
+        k_all, v_all = cache.layers[i].keys, cache.layers[i].values  # [B, Hkv, S, d], post-rotary
         for b, L in enumerate(lens):
             rows = torch.arange(S - L, S, device=dev)  # this sequence's prefill tokens (left padded)
             k = k_all[b, :, rows].transpose(0, 1).contiguous()  # [L, Hkv, d]
@@ -100,14 +105,138 @@ def test_decode_step_matches_transformers(pkg, dev, lens):
             pkg.kv_append(k, v, kv.k[i], kv.v[i], tables[b:b + 1].expand(L, -1).contiguous(),
                           torch.arange(L, dtype=torch.int32, device=dev))
     model_dec = dec.DecodeModel(dcfg, layers, kv)
-    positions = torch.tensor(lens, dtype=torch.int32, device=dev)
+    full_mask = attn_mask
+    results = []
+    for step in range(n_steps):
+        nxt = torch.randint(0, cfg.vocab_size, (B, 1), device=dev)
+        full_mask = torch.cat([full_mask, torch.ones((B, 1), dtype=torch.long, device=dev)], dim=1)
+        new_pos = torch.tensor(lens, device=dev).view(B, 1) + step
+        with torch.no_grad():
+            model(input_ids=nxt, attention_mask=full_mask, position_ids=new_pos, past_key_values=cache, use_cache=True)
+            ref = outs["last"].view(B, cfg.hidden_size)
+            emb = model.model.embed_tokens(nxt).view(B, cfg.hidden_size)
+            positions = (torch.tensor(lens, dtype=torch.int32, device=dev) + step).contiguous()
+            got = model_dec.step(emb.contiguous(), positions, positions + 1, tables)
+        torch.cuda.synchronize()
+        g, r = np_f32(got), np_f32(ref)
+        scale = float(np.abs(r).max())
+        max_abs, mean_rel = errors(g, r)
+        results.append((max_abs, mean_rel, scale))
+        assert max_abs <= max_abs_scale * max(scale, 1.0) and mean_rel <= 2e-2, (step, max_abs, mean_rel, scale)
+    return results
+
+
+@pytest.mark.parametrize("lens", [[23], [40, 17, 5]])
+def test_decode_step_matches_transformers(pkg, dev, lens):
+    cfg, model = _model(dev)
+    _compare_decode_steps(pkg, dev, cfg, model, lens, n_steps=2)
+
+
+def _compare_layers_teacher_forced(pkg, dev, cfg, model, lens, n_steps=2):
+    """Per decoder layer and decode step, with the reference's own layer input fed to both sides:
+    the attention sublayer (input_layernorm, q/k/v, q/k norm, rotary, cache append, paged attention,
+    o_proj) against transformers' ``self_attn`` output, and the MoE sublayer (residual add,
+    post_attention_layernorm, block, residual add) against the layer's output.  Feeding the
+    reference's inputs keeps a routing flip in one layer (a near-tie at the 8th expert moved by
+    bf16 noise) from propagating into the next; tokens whose expert set differs between the two
+    sides' normalised inputs are left out of the MoE comparison and counted."""
+    from transformers import DynamicCache
+
+    from inference_server_amd import decode as dec
+
+    assert pkg.swap_moe_blocks(model, quantize_fp8=True) == cfg.num_hidden_layers
+    B, S = len(lens), max(lens)
+    H, k = cfg.hidden_size, cfg.num_experts_per_tok
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev)
+    attn_mask = torch.zeros((B, S), dtype=torch.long, device=dev)
+    for b, L in enumerate(lens):
+        attn_mask[b, S - L:] = 1
+    cap = {}
+    hooks = []
+    for i, layer in enumerate(model.model.layers):
+        def pre(mod, args, kwargs, i=i):
+            hs = kwargs.get("hidden_states", args[0] if args else None)
+            cap[("in", i)] = hs.detach().clone()
+        def post(mod, args, out, i=i):
+            cap[("out", i)] = (out[0] if isinstance(out, tuple) else out).detach().clone()
+        def attn_post(mod, args, out, i=i):
+            cap[("attn", i)] = out[0].detach().clone()
+        def mlp_pre(mod, args, i=i):
+            cap[("mlp_in", i)] = args[0].detach().clone()
+        hooks += [layer.register_forward_pre_hook(pre, with_kwargs=True), layer.register_forward_hook(post),
+                  layer.self_attn.register_forward_hook(attn_post), layer.mlp.register_forward_pre_hook(mlp_pre)]
+    cache = DynamicCache()
     with torch.no_grad():
-        got = model_dec.step(emb.contiguous(), positions, positions + 1, tables)
-    torch.cuda.synchronize()
-    g, r = np_f32(got), np_f32(ref)
-    scale = float(np.abs(r).max())
-    max_abs, mean_rel = errors(g, r)
-    assert max_abs <= 2e-2 * max(scale, 1.0) and mean_rel <= 2e-2, (max_abs, mean_rel, scale)
+        pos = (attn_mask.cumsum(-1) - 1).clamp(min=0)
+        model(input_ids=ids, attention_mask=attn_mask, position_ids=pos, past_key_values=cache, use_cache=True)
+
+    dcfg = dec.DecoderConfig(hidden=H, heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads,
+                             head_dim=128, experts=cfg.num_experts, top_k=k, moe_intermediate=cfg.moe_intermediate_size,
+                             rms_eps=cfg.rms_norm_eps, rope_theta=1e6)
+    layers = [dec.DecoderLayerWeights.from_hf_layer(l, dcfg) for l in model.model.layers]
+    max_pages = (S + n_steps + PAGE - 1) // PAGE + 1
+    n_pages = B * max_pages + 2
+    kv = dec.PagedKVCache(cfg.num_hidden_layers, n_pages, cfg.num_key_value_heads, dev)
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+    tables = perm[: B * max_pages].view(B, max_pages).contiguous().to(dev)
+    for i in range(cfg.num_hidden_layers):
+        k_all, v_all = cache.layers[i].keys, cache.layers[i].values
+        for b, L in enumerate(lens):
+            rows = torch.arange(S - L, S, device=dev)
+            kk = k_all[b, :, rows].transpose(0, 1).contiguous()
+            vv = v_all[b, :, rows].transpose(0, 1).contiguous()
+            pkg.kv_append(kk, vv, kv.k[i], kv.v[i], tables[b:b + 1].expand(L, -1).contiguous(),
+                          torch.arange(L, dtype=torch.int32, device=dev))
+    inv_freq = dec.default_inv_freq(dcfg, dev)
+    full_mask = attn_mask
+    report = []
+    for step in range(n_steps):
+        nxt = torch.randint(0, cfg.vocab_size, (B, 1), device=dev)
+        full_mask = torch.cat([full_mask, torch.ones((B, 1), dtype=torch.long, device=dev)], dim=1)
+        new_pos = torch.tensor(lens, device=dev).view(B, 1) + step
+        positions = (torch.tensor(lens, dtype=torch.int32, device=dev) + step).contiguous()
+        with torch.no_grad():
+            model(input_ids=nxt, attention_mask=full_mask, position_ids=new_pos, past_key_values=cache, use_cache=True)
+            for i, w in enumerate(layers):
+                h_in = cap[("in", i)].reshape(B, H).contiguous()
+                a_ref = cap[("attn", i)].reshape(B, H).contiguous()
+                out_ref = cap[("out", i)].reshape(B, H)
+                a = dec.attention_sublayer(w, h_in, positions, positions + 1, tables, inv_freq, kv.k[i], kv.v[i])
+                ga, ra = np_f32(a), np_f32(a_ref)
+                a_max, a_rel = errors(ga, ra)
+                a_scale = float(np.abs(ra).max())
+                assert a_max <= 2e-2 * max(a_scale, 1.0) and a_rel <= 1e-2, ("attention", step, i, a_max, a_rel)
+                out = dec.moe_sublayer(w, h_in, a_ref)
+                # routing of both sides' normalised MoE inputs
+                xn = pkg.rms_norm((h_in + a_ref).contiguous(), w.ln2, dcfg.rms_eps)
+                _, _, ids_ours = pkg.route(xn, w.router, k)
+                _, _, ids_ref = pkg.route(cap[("mlp_in", i)].reshape(B, H).contiguous(), w.router, k)
+                same = [set(ids_ours[b].tolist()) == set(ids_ref[b].tolist()) for b in range(B)]
+                keep = np.array(same)
+                o_max, o_rel = errors(np_f32(out)[keep], np_f32(out_ref)[keep])
+                o_scale = float(np.abs(np_f32(out_ref)).max())
+                assert o_max <= 2e-2 * max(o_scale, 1.0) and o_rel <= 1e-2, ("moe", step, i, o_max, o_rel)
+                report.append((step, i, a_max, a_rel, o_max, o_rel, int((~keep).sum())))
+        torch.cuda.synchronize()
+    for h in hooks:
+        h.remove()
+    print("step layer attn(max, rel) moe(max, rel) routing-flips:", report)
+    # routing flips are rare events (near-ties moved by bf16 noise), not the rule
+    assert sum(r[-1] for r in report) <= max(1, len(report) * B // 8)
+    return report
+
+
+@pytest.mark.timeout(900)
+def test_decode_steps_full_shape_match_transformers(pkg, dev):
+    """BASELINE config 5's layer shape (hidden 2048, 32 q / 4 kv heads, head_dim 128, 128 experts,
+    top-8, moe_intermediate 768, FP8 experts) over three decoder layers and two decode steps, with
+    contexts from 33 to 8192 tokens (config 5 draws them from [512, 8192]; the short ones add a
+    partial single page and the one-split case), compared layer by layer."""
+    cfg, model = _model(dev, n_layers=3, heads=32, kv_heads=4, hidden=2048, experts=128, top_k=8,
+                        moe_intermediate=768, max_pos=8448)
+    _compare_layers_teacher_forced(pkg, dev, cfg, model, [8192, 3001, 517, 33], n_steps=2)
+    del model
+    torch.cuda.empty_cache()
 
 
 def test_decode_step_graph_replays_match_eager(pkg, dev):
@@ -134,3 +263,19 @@ def test_decode_step_graph_replays_match_eager(pkg, dev):
             junk = torch.randn((1024, 1024), device=dev) @ torch.randn((1024, 1024), device=dev)
             del junk
             assert torch.equal(out, eager)
+
+
+@pytest.mark.timeout(900)
+def test_decode_steps_full_shape_end_to_end(pkg, dev):
+    """The same full-shape layers run end to end (each side feeds itself) over two decode steps:
+    the last layer's hidden state within mean-relative 2e-2, the tiny-model bar.  The max-abs bar is
+    5e-2 of the hidden-state scale instead of 2e-2: with 128 experts, bf16 noise from an earlier
+    layer can move a near-tie at a token's 8th expert, so one expert's contribution (an eighth of
+    the block output) differs for that token in a later layer (measured 0.148 at scale 5.3, mean
+    1.4%).  The layer-by-layer test above separates that effect out."""
+    cfg, model = _model(dev, n_layers=3, heads=32, kv_heads=4, hidden=2048, experts=128, top_k=8,
+                        moe_intermediate=768, max_pos=8448)
+    res = _compare_decode_steps(pkg, dev, cfg, model, [8192, 3001, 517, 33], n_steps=2, max_abs_scale=5e-2)
+    print("step (max_abs, mean_rel, scale):", res)
+    del model
+    torch.cuda.empty_cache()

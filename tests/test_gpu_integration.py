@@ -76,7 +76,7 @@ def test_swapped_model_prefill_and_decode(pkg, dev):
             layer.mlp.gate.weight.normal_(0, 0.02)
             layer.mlp.experts.gate_up_proj.normal_(0, 0.02)
             layer.mlp.experts.down_proj.normal_(0, 0.02)
-    assert pkg.swap_moe_blocks(model) == cfg.num_hidden_layers
+    assert pkg.swap_moe_blocks(model, quantize_fp8=True) == cfg.num_hidden_layers
     captured = []
 
     def hook(mod, inp, out):
@@ -112,3 +112,115 @@ def test_swapped_model_prefill_and_decode(pkg, dev):
                               e.down_proj_scale_inv.cpu().numpy())
         max_abs, mean_rel = errors(np_f32(y).reshape(ref.shape), ref)
         assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
+
+
+def _tiny_model(dev, **kw):
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeForCausalLM
+
+    torch.manual_seed(0)
+    cfg = _tiny_config(**kw)
+    model = Qwen3MoeForCausalLM(cfg).to(torch.bfloat16).to(dev).eval()
+    with torch.no_grad():
+        for layer in model.model.layers:
+            layer.mlp.gate.weight.normal_(0, 0.02)
+            layer.mlp.experts.gate_up_proj.normal_(0, 0.02)
+            layer.mlp.experts.down_proj.normal_(0, 0.02)
+    return cfg, model
+
+
+def test_graphed_swap_replays_match_oracle(pkg, dev):
+    """swap_moe_blocks(graphed=True): decode batches replay a captured graph per bucket.  Every
+    replayed block output is checked against the oracle on the block's own routing, and equals the
+    eager block bit for bit."""
+    from transformers import DynamicCache
+
+    cfg, model = _tiny_model(dev)
+    assert pkg.swap_moe_blocks(model, quantize_fp8=True, graphed=True) == cfg.num_hidden_layers
+    captured = []
+
+    def hook(mod, inp, out):
+        captured.append((mod, inp[0].detach().clone(), out.detach().clone()))
+
+    for layer in model.model.layers:
+        assert isinstance(layer.mlp, pkg.MI355XGraphedMoeBlock)
+        layer.mlp.register_forward_hook(hook)
+    B, S = 5, 12  # decode batch 5 pads to the 8-token bucket
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev)
+    cache = DynamicCache()
+    with torch.no_grad():
+        out = model(input_ids=ids, past_key_values=cache, use_cache=True)  # 60 tokens: bucket 64
+        nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+        for _ in range(2):  # two decode steps: the second replays the graphs captured by the first
+            out = model(input_ids=nxt, past_key_values=cache, use_cache=True)
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    assert len(captured) == 3 * cfg.num_hidden_layers
+    assert all(8 in m._graphs and 64 in m._graphs for m in {id(m): m for m, _, _ in captured}.values())
+    for mod, x, y in captured:
+        blk = mod.block
+        xs = x.reshape(-1, cfg.hidden_size)
+        eager, (glg, gw, gids) = pkg.moe_block_fp8(xs, blk.gate.weight, cfg.num_experts_per_tok,
+                                                   blk.experts.gate_up_proj, blk.experts.gate_up_proj_scale_inv,
+                                                   blk.experts.down_proj, blk.experts.down_proj_scale_inv,
+                                                   return_routing=True)
+        assert torch.equal(y.reshape(eager.shape), eager)
+        ids_ref, w_ref, _ = orc.topk_from_logits(np_f32(glg), cfg.num_experts_per_tok)
+        np.testing.assert_array_equal(gids.cpu().numpy(), ids_ref)
+        e = blk.experts
+        ref = orc.experts_fp8(np_f32(xs), ids_ref, w_ref, f8_codes(e.gate_up_proj),
+                              e.gate_up_proj_scale_inv.cpu().numpy(), f8_codes(e.down_proj),
+                              e.down_proj_scale_inv.cpu().numpy())
+        max_abs, mean_rel = errors(np_f32(y).reshape(ref.shape), ref)
+        assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL
+
+
+def test_graphed_block_crossing_tile_switch(pkg, dev):
+    """E = 100, k = 6: the tile height changes at 8 E / k = 133.3 tokens, inside the default
+    (128, 256] bucket.  The bucket list gains an edge at 133, so 129..133 tokens (16-row tiles)
+    and 134 tokens (32-row tiles) each replay a graph of their own tiling, bit-equal to eager."""
+    E, H, I, k = 100, 512, 256, 6
+    block = pkg.MI355XSparseMoeBlock(E, H, I, k, device=dev)
+    g = torch.Generator(device=dev).manual_seed(21)
+    with torch.no_grad():
+        block.gate.weight.copy_((torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        from tests.helpers import gpu_weights
+
+        for name, t in zip(("gate_up_proj", "gate_up_proj_scale_inv", "down_proj", "down_proj_scale_inv"),
+                           gpu_weights(E, H, I, dev, seed=22)):
+            getattr(block.experts, name).copy_(t)
+    graphed = pkg.MI355XGraphedMoeBlock(block)
+    assert 133 in graphed.buckets
+    for T in (130, 133, 134, 200):
+        x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+        want = block(x)
+        got = graphed(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), T
+
+
+def test_compiled_swapped_model_matches_eager(pkg, dev):
+    """The reference compiles the whole model when COMPILE_MODEL is set (torch_backend.py:44-47).
+    The swapped blocks call torch.ops.moe_mi355x.*, so Dynamo traces through them: the prefill and a
+    decode step of torch.compile(model, fullgraph=True) equal the eager model bit for bit."""
+    from transformers import DynamicCache
+
+    cfg, model = _tiny_model(dev)
+    assert pkg.swap_moe_blocks(model, quantize_fp8=True) == cfg.num_hidden_layers
+    B, S = 2, 10
+    ids = torch.randint(0, cfg.vocab_size, (B, S), device=dev)
+
+    def step(input_ids, cache):
+        return model(input_ids=input_ids, past_key_values=cache, use_cache=True).logits
+
+    compiled = torch.compile(step, backend="aot_eager", fullgraph=True)
+    with torch.no_grad():
+        cache_e, cache_c = DynamicCache(), DynamicCache()
+        want = step(ids, cache_e)
+        got = compiled(ids, cache_c)
+        assert torch.equal(got, want)
+        nxt = want[:, -1].argmax(-1, keepdim=True)  # one decode step on the KV cache
+        want1 = step(nxt, cache_e)
+        got1 = compiled(nxt, cache_c)
+        assert got1.shape == (B, 1, cfg.vocab_size)
+        assert torch.equal(got1, want1)
+    torch.cuda.synchronize()

@@ -170,7 +170,7 @@ def w30b(dev):
     return gpu_weights(128, 2048, 768, dev, seed=0)
 
 
-@pytest.mark.parametrize("T", [1, 8, 32, 64, 256])
+@pytest.mark.parametrize("T", [1, 8, 32, 64, 128, 256])
 def test_experts_decode_30b(pkg, dev, w30b, T):
     rng = np.random.default_rng(10 + T)
     x = orc.gen_normal_bf16(rng, (T, 2048))
@@ -179,7 +179,8 @@ def test_experts_decode_30b(pkg, dev, w30b, T):
 
 
 def test_experts_prefill_skewed_30b(pkg, dev, w30b):
-    """4096-token chunk with Zipf-skewed routing; 96 sampled tokens checked (tokens are independent)."""
+    """4096-token chunk with Zipf-skewed routing; 96 random tokens checked (tokens are independent;
+    tests/test_gpu_configs.py checks a token of every tile)."""
     T, H, E, k = 4096, 2048, 128, 8
     rng = np.random.default_rng(11)
     x = orc.gen_normal_bf16(rng, (T, H))

@@ -182,6 +182,28 @@ def test_align_brute_force():
     assert tl[:, 2].sum() == T * k and np.all(tl[:, 2] <= 4)
 
 
+@pytest.mark.parametrize("block_m", [1, 4, 16, 128])
+def test_tile_list_brute_force(block_m):
+    """tile_list against a sequential scan of the sorted expert column: a new tile starts where the
+    expert changes or the current tile is full.  Pins every tile's expert, start row and length."""
+    rng = np.random.default_rng(9 + block_m)
+    for T, k, E in ((37, 3, 9), (300, 8, 16), (5, 2, 40), (0, 4, 3)):
+        ids = rng.integers(0, E, size=(T, k))
+        if T > 10:
+            ids[: T // 2, 0] = 2  # a hot expert: several full tiles then a remainder
+        _, counts, _ = orc.align(ids, E)
+        sorted_e = np.sort(ids.reshape(-1), kind="stable")
+        expect = []
+        for row, e in enumerate(sorted_e):
+            if expect and expect[-1][0] == e and expect[-1][2] < block_m:
+                expect[-1][2] += 1
+            else:
+                expect.append([int(e), row, 1])
+        got = orc.tile_list(counts, block_m)
+        assert got.shape == (len(expect), 3)
+        np.testing.assert_array_equal(got, np.array(expect, dtype=np.int32).reshape(-1, 3))
+
+
 # ---------------------------------------------------------------------------
 # experts
 # ---------------------------------------------------------------------------
