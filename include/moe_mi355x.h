@@ -34,6 +34,7 @@ enum {
   MOE_ERR_INVALID_ARG = -1,    /* null pointer, bad size or unsupported shape */
   MOE_ERR_WORKSPACE = -2,      /* workspace smaller than *_workspace_bytes() */
   MOE_ERR_ALIGNMENT = -3,      /* a pointer is not 16-byte aligned */
+  MOE_ERR_SCRATCH = -4,        /* larger than the no-allocation entry point's fixed scratch */
 };
 
 /* Human-readable text for a return code (MOE_ERR_* or hipError_t). */
@@ -125,6 +126,22 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
                          int renorm, const void* w13, const float* s13, const void* w2,
                          const float* s2, void* out, void* logits, void* ids, int id_bytes,
                          void* weights, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * moe_mi355x_block_fp8 without a workspace argument and without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Its scratch is a fixed device array inside the library,
+ * moe_mi355x_block_fp8_noalloc_scratch_bytes() = 64 MiB, one per GPU, held until the process ends
+ * (enough for moe_mi355x_block_workspace_bytes of decode batches up to 256 tokens at the
+ * Qwen3-235B-A22B shape, or 1024 at Qwen3-30B-A3B); a call needing more returns MOE_ERR_SCRATCH
+ * and launches nothing.  Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams or two threads at once) race.  Results are identical to moe_mi355x_block_fp8's.
+ */
+size_t moe_mi355x_block_fp8_noalloc_scratch_bytes(void);
+int moe_mi355x_block_fp8_noalloc(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                                 int renorm, const void* w13, const float* s13, const void* w2,
+                                 const float* s2, void* out, void* logits, void* ids, int id_bytes,
+                                 void* weights, void* stream);
 
 /*
  * Which of the block path's batch-size-dependent launch choices can change its output bits

@@ -4,6 +4,8 @@
 //
 // Reference: fp8_grouped_mm_experts_forward, TF/integrations/finegrained_fp8.py:498-589,
 // and Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
+#include <mutex>
+
 #include "common.h"
 
 int moe_gemm_block_m(int S, int E, int H, int I);
@@ -192,6 +194,9 @@ extern "C" const char* moe_mi355x_error_string(int code) {
     case MOE_ERR_INVALID_ARG: return "invalid argument (null pointer, size or unsupported shape)";
     case MOE_ERR_WORKSPACE: return "workspace missing or smaller than the *_workspace_bytes() size";
     case MOE_ERR_ALIGNMENT: return "a tensor pointer is not 16-byte aligned";
+    case MOE_ERR_SCRATCH:
+      return "the call needs more scratch than the no-allocation entry point's fixed device buffer holds "
+             "(moe_mi355x_block_fp8_noalloc_scratch_bytes); use moe_mi355x_block_fp8 with a workspace";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }
@@ -331,4 +336,64 @@ extern "C" int moe_mi355x_moe_sublayer_fp8(const void* h, const void* h_add, con
   if (rc) return rc;
   return block_impl(xn, w_router, T, H, I, E, k, renorm, w13, s13, w2, s2, out, nullptr, nullptr, 4, nullptr, b, s,
                     h_add ? hs : h);
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation variant of moe_mi355x_block_fp8 for callers that cannot allocate (code under HIP
+// graph capture, tight serving loops).  Its scratch is this file-scope device array: one copy per
+// GPU the library runs on, held until the process ends.  Host code never passes the array's name
+// to a kernel (on the host it is a stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device on that device's first call, and is kept per device.
+// Every call on a GPU shares that GPU's array, so calls that overlap on one GPU (two streams, two
+// threads) race; nothing in it has to start at zero (every kernel writes what it later reads, and
+// the router clears the sort's histogram slots itself).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's scratch array (looked up on the device's first call).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return MOE_ERR_INVALID_ARG;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return MOE_ERR_INVALID_ARG;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+}  // namespace
+
+extern "C" size_t moe_mi355x_block_fp8_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int moe_mi355x_block_fp8_noalloc(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                                            int renorm, const void* w13, const float* s13, const void* w2,
+                                            const float* s2, void* out, void* logits, void* ids, int id_bytes,
+                                            void* weights, void* stream) {
+  MOE_RETURN_IF(!experts_args_ok(T, H, I, E, k, id_bytes), MOE_ERR_INVALID_ARG);
+  if (T == 0) return MOE_OK;
+  MOE_RETURN_IF(!x || !w_router || !w13 || !s13 || !w2 || !s2 || !out, MOE_ERR_INVALID_ARG);
+  MOE_RETURN_IF(!experts_aligned(x, w13, w2, out) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
+  const size_t need = carve_block(nullptr, T, H, I, E, k).total;
+  MOE_RETURN_IF(need > kNoAllocScratchBytes, MOE_ERR_SCRATCH);
+  void* base = nullptr;
+  const int rc = scratch_for_current_device(&base);
+  if (rc) return rc;
+  const BlockWs b = carve_block(base, T, H, I, E, k);
+  return block_impl(x, w_router, T, H, I, E, k, renorm, w13, s13, w2, s2, out, logits, ids, id_bytes, weights, b,
+                    (hipStream_t)stream, nullptr);
 }
