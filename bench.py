@@ -62,9 +62,14 @@ class Shape:
 
     def gate_up_bytes(self, n_active, T):
         """Algorithmic HBM bytes of one gate_up launch: the active experts' W13 + scales,
-        the fp8 activations and their scales read, the bf16 intermediate written."""
-        return (n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128)
-                + 2 * T * K_TOP * self.I)
+        the fp8 activations and their scales read, the intermediate written (on 16-row tiles,
+        S <= 8 E, the launch quantises it itself: e4m3 codes + scales, and its bf16 h
+        round trip between the launch's workgroups is counted too; otherwise bf16 h)."""
+        S = T * K_TOP
+        out = 2 * S * self.I
+        if S <= 8 * self.E:
+            out += 2 * S * self.I + S * self.I + 4 * S * (self.I // 128)
+        return n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128) + out
 
     def gate_up_flops(self, T):
         return 2.0 * T * K_TOP * (2 * self.I) * self.H

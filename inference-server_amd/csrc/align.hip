@@ -20,7 +20,8 @@ namespace {
 __global__ __launch_bounds__(kChunk) void align_single_kernel(const void* ids, int id_bytes, int S, int E,
                                                               int block_m, int32_t* perm, int32_t* counts,
                                                               int32_t* offsets, int32_t* tiles,
-                                                              int32_t* n_tiles) {
+                                                              int32_t* n_tiles, int32_t* zero, int nzero) {
+  zero_counters(zero, nzero);
   __shared__ int s_cnt[kBuckets];
   __shared__ int s_off[kBuckets];
   __shared__ int s_toff[kBuckets];
@@ -55,7 +56,8 @@ __global__ __launch_bounds__(kChunk) void align_scan_scatter_kernel(const void* 
                                                                     int block_m, const int32_t* __restrict__ bc,
                                                                     int nb, int32_t* perm, int32_t* counts,
                                                                     int32_t* offsets, int32_t* tiles,
-                                                                    int32_t* n_tiles) {
+                                                                    int32_t* n_tiles, int32_t* zero, int nzero) {
+  if (blockIdx.x == 0) zero_counters(zero, nzero);
   __shared__ int s_cnt[kBuckets];
   __shared__ int s_off[kBuckets];
   __shared__ int s_toff[kBuckets];
@@ -97,14 +99,15 @@ extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E) {
 
 int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
                              int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                             hipStream_t s);
+                             hipStream_t s, int32_t* zero, int nzero);
 
+// `zero` / `nzero`: counters of the grouped GEMMs' hand-offs, cleared by the align kernel.
 int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
                      int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles, void* workspace,
-                     size_t workspace_bytes, hipStream_t s) {
+                     size_t workspace_bytes, hipStream_t s, int32_t* zero, int nzero) {
   if (S <= kSingleMaxS) {
     MOE_LAUNCH(MOE_PROF_ALIGN, s, align_single_kernel, dim3(1), dim3(kChunk), 0, s, ids, id_bytes, S, E, block_m, perm,
-                       counts, offsets, tiles, n_tiles);
+                       counts, offsets, tiles, n_tiles, zero, nzero);
     MOE_CHECK_LAUNCH();
     return MOE_OK;
   }
@@ -113,17 +116,18 @@ int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, i
   int32_t* bc = (int32_t*)workspace;
   MOE_LAUNCH(MOE_PROF_ALIGN, s, align_count_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E, bc);
   MOE_CHECK_LAUNCH();
-  return moe_launch_align_counted(ids, id_bytes, S, E, block_m, bc, perm, counts, offsets, tiles, n_tiles, s);
+  return moe_launch_align_counted(ids, id_bytes, S, E, block_m, bc, perm, counts, offsets, tiles, n_tiles, s, zero,
+                                  nzero);
 }
 
 // The rest of the large-S align once the chunk histograms bc [nb, E + 1] are filled (by
 // align_count_kernel, or by the top-k kernel of the block path).
 int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
                              int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                             hipStream_t s) {
+                             hipStream_t s, int32_t* zero, int nzero) {
   const int nb = (S + kChunk - 1) / kChunk;
   MOE_LAUNCH(MOE_PROF_ALIGN, s, align_scan_scatter_kernel, dim3(nb), dim3(kChunk), 0, s, ids, id_bytes, S, E,
-             block_m, bc, nb, perm, counts, offsets, tiles, n_tiles);
+             block_m, bc, nb, perm, counts, offsets, tiles, n_tiles, zero, nzero);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -139,5 +143,5 @@ extern "C" int moe_mi355x_align(const void* ids, int id_bytes, int T, int k, int
   MOE_RETURN_IF(S > 0 && (!ids || !perm || !tiles), MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!moe_aligned16(tiles), MOE_ERR_ALIGNMENT);
   return moe_launch_align(ids, id_bytes, (int)S, E, block_m, perm, counts, offsets, tiles, n_tiles, workspace,
-                          workspace_bytes, (hipStream_t)stream);
+                          workspace_bytes, (hipStream_t)stream, nullptr, 0);
 }

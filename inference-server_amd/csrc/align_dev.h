@@ -56,6 +56,12 @@ __device__ void scan_counts(const int* s_cnt, int E, int block_m, int* s_off, in
   }
 }
 
+// Zeroes the n counters at `zero` (the grouped GEMMs' hand-off counters, which the align of the
+// same call clears so that no earlier call can leave them dirty).
+__device__ __forceinline__ void zero_counters(int32_t* zero, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) zero[i] = 0;
+}
+
 // Writes counts, offsets and the tile list from the scanned LDS arrays.
 __device__ void emit_meta(const int* s_cnt, const int* s_off, const int* s_toff, int E, int block_m,
                           int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles) {

@@ -40,6 +40,17 @@ struct GemmArgs {
   int K;                   // reduction length
   int N;                   // output columns (gate_up: I, down: H)
   int topk;                // k, for pair -> token
+  // Hand-offs inside the launch (null: off).  gate_up: the last workgroup of a (tile, 128-column
+  // group) to finish quantises that group of the tile's h rows into hq / sh (tile_cnt
+  // [max_tiles, N / 128], zero on entry).  down: the
+  // last of a token's k pair rows to finish a column block sums the token's k rows of that block
+  // in slot order into comb (tok_cnt [T, column blocks], zero on entry; every id must be valid).
+  int32_t* tile_cnt;
+  uint8_t* hq;
+  float* sh;
+  int32_t* tok_cnt;
+  uint16_t* comb;
+  const uint16_t* residual;  // down: comb = bf16(residual + bf16(sum)) when non-null
 };
 
 constexpr int kMaxKB = 32;  // K <= 4096
@@ -76,6 +87,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
   // conflict-free
   __shared__ __attribute__((aligned(16))) uint4 s_at[SHA ? 2 : 1][SHA ? BM * 8 : 1];
   static_assert(!SHA || (KS == 1 && BM * 8 == 256), "SHA stages one 16-byte chunk per thread, no K split");
+  __shared__ int s_done;     // result waves past their hand-off stores
+  __shared__ int s_tok[BM];  // down hand-off: tokens this workgroup combines
+  if (threadIdx.x == 0) s_done = 0;  // visible after the barriers of the row setup below
 
   // The weight stream needs only the expert and the column block: its first loads go
   // out before the activation-row setup (perm -> rows -> scales), whose dependent round
@@ -196,6 +210,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
     }
   }
 
+  // after the K-split reduction only the ks == 0 waves hold sums; the others leave, freeing their
+  // slots for the next workgroups
   if constexpr (KS > 1) {
     constexpr int PER = WM * NOP * 4;
     if (ks > 0) {
@@ -221,23 +237,143 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
     }
   }
 
+  const bool handoff = MODE == MODE_GATE_UP ? p.tile_cnt != nullptr : p.tok_cnt != nullptr;  // uniform
   const int col = n0 + lr;
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi) {
+    // one bf16 per (row 4 lg + q, column lr) and output slice o
+    uint32_t v[NOP][4];
+    int dst_row[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = mi * 16 + 4 * lg + q;
-      if (r >= rows) continue;
-      const int srow = row0 + r;
+      const int srow = row0 + min(r, rows - 1);
       if constexpr (MODE == MODE_GATE_UP) {
-        p.out[(long)srow * p.N + col] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
+        v[0][q] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
+        dst_row[q] = srow;
       } else {
         const int pair = p.perm[srow];
         const float wt = bf16_to_f32(p.topk_w[pair]);
 #pragma unroll
-        for (int o = 0; o < NOP; ++o)
-          p.out[(long)pair * p.N + col + 16 * o] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
+        for (int o = 0; o < NOP; ++o) v[o][q] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
+        dst_row[q] = pair;
       }
+    }
+    constexpr int NV = MODE == MODE_GATE_UP ? 1 : NOP;
+    if (!handoff) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (mi * 16 + 4 * lg + q >= rows) continue;
+#pragma unroll
+        for (int o = 0; o < NV; ++o) p.out[(long)dst_row[q] * p.N + col + 16 * o] = (uint16_t)v[o][q];
+      }
+    } else {
+      // device-coherent stores for the wave that finishes the group / token: lanes lr and lr ^ 1
+      // hold adjacent columns of the same rows, so the even lane stores rows q = 0, 1 and the odd
+      // lane rows 2, 3, each as one 32-bit store of both columns
+      const bool odd = lr & 1;
+#pragma unroll
+      for (int o = 0; o < NV; ++o) {
+        uint32_t pv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pv[q] = (uint32_t)__shfl_xor((int)v[o][q], 1);
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int q = odd ? 2 + h2 : h2;
+          if (mi * 16 + 4 * lg + q >= rows) continue;
+          const uint32_t both = odd ? (pv[q] | (v[o][q] << 16)) : (v[o][q] | (pv[q] << 16));
+          xwg_store32(p.out + (long)dst_row[q] * p.N + (col & ~1) + 16 * o, both);
+        }
+      }
+    }
+  }
+  if (!handoff) return;
+  // The CG result waves of the workgroup each wait for their stores; the last of them to get
+  // there counts the workgroup in (an LDS counter elects it), the others leave.
+  xwg_wait_stores();
+  int order = 0;
+  if (lane == 0) order = atomicAdd(&s_done, 1);
+  order = __builtin_amdgcn_readfirstlane(order);
+  if (order != CG - 1) return;
+
+  if constexpr (MODE == MODE_GATE_UP) {
+    // per (tile, 128-column group of h): the last of the group's 128 / (16 CG) workgroups to count
+    // in quantises the group for the tile's rows (16 lanes per row, 8 rows in flight per batch)
+    constexpr int WG_COLS = 16 * CG;
+    const int G = p.N / MOE_GROUP;
+    const int gi = blockIdx.x * WG_COLS / MOE_GROUP;
+    int last = 0;
+    if (lane == 0) last = xwg_count_in(p.tile_cnt + (long)tile * G + gi) == MOE_GROUP / WG_COLS - 1;
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    const int sub = lane & 15, grp = lane >> 4;  // 4 rows at a time
+    for (int r0 = grp; r0 < rows; r0 += 32) {
+      uint4 hv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = min(r0 + 4 * i, rows - 1);
+        hv[i] = xwg_load128(p.out + (long)(row0 + r) * p.N + gi * MOE_GROUP + sub * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = r0 + 4 * i;
+        if (r >= rows) break;  // uniform over the 16 lanes of a row
+        const long e0 = (long)(row0 + r) * p.N + gi * MOE_GROUP + sub * 8;
+        quant_group16_raw(hv[i], p.hq + e0, p.sh + (long)(row0 + r) * G + gi, sub);
+      }
+    }
+  } else {
+    // one tile row (pair) per lane counts in for its token's column block; the lanes whose count
+    // completes the token's k slots list their tokens, and this wave sums each listed token's k
+    // rows over the workgroup's columns: fp32 in slot order, the residual add, one bf16 rounding
+    static_assert(BM <= MOE_WAVE, "one tile row per lane");
+    bool done = false;
+    int t = 0;
+    if (lane < rows) {
+      t = p.perm[row0 + lane] / p.topk;
+      done = xwg_count_in(p.tok_cnt + (long)t * gridDim.x + blockIdx.x) == p.topk - 1;
+    }
+    const uint64_t mask = __ballot(done);
+    if (done) s_tok[__popcll(mask & lanemask_lt())] = t;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const int ntok = __popcll(mask);
+    constexpr int CB = CG * WCOLS;  // this workgroup's output columns
+    constexpr int PER_TOK = CB / 8;
+    for (int u = lane; u < ntok * PER_TOK; u += MOE_WAVE) {
+      const int tt = s_tok[u / PER_TOK];
+      const int c0 = blockIdx.x * CB + (u % PER_TOK) * 8;
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j0 = 0; j0 < p.topk; j0 += 8) {
+        uint4 rv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          rv[j] = xwg_load128(p.out + (long)(tt * p.topk + min(j0 + j, p.topk - 1)) * p.N + c0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j0 + j >= p.topk) break;
+          const uint32_t w4[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            sum[2 * i] += __uint_as_float(w4[i] << 16);
+            sum[2 * i + 1] += __uint_as_float(w4[i] & 0xffff0000u);
+          }
+        }
+      }
+      if (p.residual != nullptr) {
+        const uint4 r4 = *(const uint4*)(p.residual + (long)tt * p.N + c0);
+        const uint32_t ru[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sum[2 * i] = __uint_as_float(ru[i] << 16) + round_bf16(sum[2 * i]);
+          sum[2 * i + 1] = __uint_as_float(ru[i] & 0xffff0000u) + round_bf16(sum[2 * i + 1]);
+        }
+      }
+      uint4 o4;
+      o4.x = (uint32_t)f32_to_bf16(sum[0]) | ((uint32_t)f32_to_bf16(sum[1]) << 16);
+      o4.y = (uint32_t)f32_to_bf16(sum[2]) | ((uint32_t)f32_to_bf16(sum[3]) << 16);
+      o4.z = (uint32_t)f32_to_bf16(sum[4]) | ((uint32_t)f32_to_bf16(sum[5]) << 16);
+      o4.w = (uint32_t)f32_to_bf16(sum[6]) | ((uint32_t)f32_to_bf16(sum[7]) << 16);
+      *(uint4*)(p.comb + (long)tt * p.N + c0) = o4;
     }
   }
 }
@@ -275,15 +411,29 @@ int moe_gemm_block_m(int S, int E, int H, int I) {
   return H % 256 == 0 && H >= 512 && I >= 512 ? 128 : 64;
 }
 
+// Column blocks of the decode down GEMM for S pairs at tile height block_m: the width of the
+// per-token hand-off counters (tok_cnt [T, blocks]).
+int moe_down_col_blocks(int S, int H, int block_m) {
+  if (block_m == 16) return S > 64 ? H / 64 : H / 32;  // CG 2 x 16 DN columns
+  if (block_m == 32) return H / 128;                   // CG 4 x 32 columns
+  return H / 64;                                       // CG 4 x 16 columns
+}
+
+// Decode-tile GEMMs (block_m 16 / 32 / 64) or the prefill GEMMs (128).  Decode tiles: with
+// tile_cnt (max_tiles x I/128 counters, zero on entry) gate_up quantises h itself and no quant_h launch
+// follows; with tok_cnt (T x moe_down_col_blocks counters, zero on entry) the down GEMM also sums
+// each token's pair rows into comb (+ residual), and no combine launch is needed.
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
                              const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
                              uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
-                             int block_m, hipStream_t s) {
+                             int block_m, hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
+                             const uint16_t* residual) {
   if (block_m == 128)
     return moe_launch_grouped_gemms_prefill(xq, sx, w13, s13, w2, s2, perm, tiles, n_tiles, max_tiles, topk_w, hq,
                                             sh, pairs, H, I, k, s);
-  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k};
+  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh,
+              nullptr, nullptr, nullptr};
   int rc;
   if (block_m == 16)
     rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
@@ -292,11 +442,14 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
-  // one pass quantises h; quantising it inside the down GEMM instead would repeat the
-  // work in every one of the H/16 column waves that read a row
-  rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
-  if (rc) return rc;
-  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
+  if (tile_cnt == nullptr) {
+    // one pass quantises h; quantising it inside the down GEMM instead would repeat the
+    // work in every one of the H/16 column waves that read a row
+    rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
+    if (rc) return rc;
+  }
+  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, nullptr, nullptr, nullptr,
+              tok_cnt, comb, residual};
   if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
     rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
   else if (block_m == 32)

@@ -9,19 +9,21 @@
 #include "common.h"
 
 int moe_gemm_block_m(int S, int E, int H, int I);
+int moe_down_col_blocks(int S, int H, int block_m);
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
                              const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint16_t* h,
                              uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
-                             int block_m, hipStream_t s);
+                             int block_m, hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
+                             const uint16_t* residual);
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
                      int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                     int32_t* chunk_counts);
+                     int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt);
 int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
                              int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                             hipStream_t s);
+                             hipStream_t s, int32_t* zero, int nzero);
 extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E);
 bool moe_route_can_fuse_align(int T, int E, int k);
 extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m);
@@ -116,6 +118,8 @@ struct ExpertsWs {
   uint8_t* hq;
   float* sh;
   uint16_t* pairs;
+  int32_t* cnt;    // 16-row tiles: the GEMMs' hand-off counters, [max_tiles, I/128] then [T, down column blocks]
+  int n_cnt;       // 0 on the other paths
   size_t total;
   int block_m;
   int max_tiles;
@@ -140,6 +144,8 @@ ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   w.hq = c.take<uint8_t>((size_t)S * I);
   w.sh = c.take<float>((size_t)S * (I / MOE_GROUP));
   w.pairs = c.take<uint16_t>((size_t)S * H);
+  w.n_cnt = w.block_m != 16 ? 0 : w.max_tiles * (I / MOE_GROUP) + T * moe_down_col_blocks(S, H, w.block_m);
+  w.cnt = c.take<int32_t>(w.n_cnt);
   w.total = moe_align_up(c.off, 256);
   return w;
 }
@@ -151,23 +157,35 @@ bool experts_args_ok(int T, int H, int I, int E, int k, int id_bytes) {
 }
 
 // Experts after routing.  `prepared` = x already quantised into w.xq/w.sx and the align
-// outputs already written (the block path fuses both into its routing kernels).
+// outputs already written, hand-off counters cleared (the block path fuses all of it into its
+// routing kernels).  `ids_valid`: every id is in [0, E) (the block path's own routing), so on
+// decode tiles the down GEMM combines each token itself; caller ids may hold expert-parallel
+// sentinels and go through the combine kernel.
 int launch_experts(const void* x, const void* ids, int id_bytes, const void* weights, int T, int H, int I,
                    int E, int k, const void* w13, const float* s13, const void* w2, const float* s2, void* out,
-                   const ExpertsWs& w, hipStream_t s, bool prepared = false, const void* residual = nullptr) {
+                   const ExpertsWs& w, hipStream_t s, bool prepared = false, const void* residual = nullptr,
+                   bool ids_valid = false) {
   const int S = T * k;
   int rc;
   if (!prepared) {
     rc = moe_launch_quant_act(x, T, H, w.xq, w.sx, s);
     if (rc) return rc;
     rc = moe_launch_align(ids, id_bytes, S, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
-                          w.align_ws, w.align_ws_bytes, s);
+                          w.align_ws, w.align_ws_bytes, s, w.cnt, w.n_cnt);
     if (rc) return rc;
   }
+  // the hand-offs pay on 16-row tiles (batches up to 8 pairs per expert): fewer launches outweigh
+  // each workgroup's wait for its stores; on 32-row tiles the separate launches are faster
+  // (Qwen3-30B-A3B layer at 256 tokens: 163 against 172 us)
+  const bool decode = w.block_m == 16;
+  const bool fused_combine = decode && ids_valid;
   rc = moe_launch_grouped_gemms(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2, w.perm, w.tiles,
                                 w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.hq, w.sh, w.pairs, S, H,
-                                I, k, w.block_m, s);
+                                I, k, w.block_m, s, decode ? w.cnt : nullptr,
+                                fused_combine ? w.cnt + (long)w.max_tiles * (I / MOE_GROUP) : nullptr, (uint16_t*)out,
+                                (const uint16_t*)residual);
   if (rc) return rc;
+  if (fused_combine) return MOE_OK;
   const long threads = (long)T * (H / 8);
   MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      (const uint16_t*)w.pairs, ids, id_bytes,
@@ -270,18 +288,19 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
   const bool counted = !fused && w.align_ws_bytes > 0;
   int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s,
                             w.xq, w.sx, w.block_m, fused ? w.perm : nullptr, w.counts, w.offsets, w.tiles,
-                            w.n_tiles, counted ? (int32_t*)w.align_ws : nullptr);
+                            w.n_tiles, counted ? (int32_t*)w.align_ws : nullptr, w.cnt, w.n_cnt);
   if (rc) return rc;
   if (counted) {
     rc = moe_launch_align_counted(id_out, idb, T * k, E, w.block_m, (const int32_t*)w.align_ws, w.perm, w.counts,
-                                  w.offsets, w.tiles, w.n_tiles, s);
+                                  w.offsets, w.tiles, w.n_tiles, s, w.cnt, w.n_cnt);
     if (rc) return rc;
   } else if (!fused) {
     rc = moe_launch_align(id_out, idb, T * k, E, w.block_m, w.perm, w.counts, w.offsets, w.tiles, w.n_tiles,
-                          w.align_ws, w.align_ws_bytes, s);
+                          w.align_ws, w.align_ws_bytes, s, w.cnt, w.n_cnt);
     if (rc) return rc;
   }
-  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s, /*prepared=*/true, residual);
+  return launch_experts(x, id_out, idb, wt, T, H, I, E, k, w13, s13, w2, s2, out, w, s, /*prepared=*/true, residual,
+                        /*ids_valid=*/true);
 }
 }  // namespace
 

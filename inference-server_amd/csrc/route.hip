@@ -346,7 +346,9 @@ __global__ __launch_bounds__(kChunk) void topk_align_kernel(const float* __restr
                                                             uint16_t* __restrict__ logits_out, void* ids,
                                                             int id_bytes, uint16_t* __restrict__ weights,
                                                             int block_m, int32_t* perm, int32_t* counts,
-                                                            int32_t* offsets, int32_t* tiles, int32_t* n_tiles) {
+                                                            int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
+                                                            int32_t* gemm_cnt, int n_gemm_cnt) {
+  zero_counters(gemm_cnt, n_gemm_cnt);  // the grouped GEMMs' hand-off counters
   __shared__ uint16_t s_lg[kFusedMaxLogits];
   __shared__ int s_ids[kSingleMaxS];
   __shared__ int s_cnt[kBuckets];
@@ -451,7 +453,7 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
                      int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                     int32_t* chunk_counts) {
+                     int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt) {
   if (T == 0) return MOE_OK;
   const bool quant = xq != nullptr;
   MOE_RETURN_IF(chunk_counts != nullptr && perm != nullptr, MOE_ERR_INVALID_ARG);
@@ -477,7 +479,7 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   if (perm != nullptr) {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_align_kernel, dim3(1), dim3(kChunk), 0, s, part, ks_eff, T, E, k, renorm,
                (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights, block_m, perm, counts, offsets, tiles,
-               n_tiles);
+               n_tiles, gemm_cnt, n_gemm_cnt);
   } else {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
                (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights,
@@ -496,7 +498,7 @@ extern "C" int moe_mi355x_route(const void* x, const void* w_router, int T, int 
   MOE_RETURN_IF(!moe_aligned16(x) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
   return moe_launch_route(x, w_router, T, H, E, k, renorm, logits, ids, id_bytes, weights, workspace,
                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, 0, nullptr, nullptr, nullptr,
-                          nullptr, nullptr, nullptr);
+                          nullptr, nullptr, nullptr, nullptr, 0);
 }
 
 extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, int renorm, void* ids,
