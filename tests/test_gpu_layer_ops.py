@@ -131,3 +131,38 @@ def test_moe_sublayer_with_attention_residual(pkg, dev, T):
     sep = pkg.moe_sublayer_fp8(h + o, ln, 1e-6, wr, k, q13, s13, q2, s2)
     torch.cuda.synchronize()
     assert torch.equal(fused, sep)
+
+
+@pytest.mark.parametrize("T", [1, 8, 64, 128])
+def test_moe_sublayer_prologue_matches_oracle(pkg, dev, T):
+    """The MoE sublayer at the Qwen3-30B-A3B shape, whose residual add, post-attention RMSNorm,
+    router GEMM and x quantisation run in one launch for decode batches, against the oracle:
+    hs = bf16(h + o), x = attn_oracle.rms_norm(hs, w_ln), moe_oracle's router and FP8 experts
+    on x, then bf16(hs + block).  Tokens whose oracle logits have a near-tie at the top-k
+    boundary (the 8th and 9th logits within 1 bf16 ulp) are left out: one ulp of RMSNorm or
+    router rounding may route them to the other expert.  With 128 experts whose logits are
+    ~N(0, 0.9), the 8th / 9th gap is within one ulp for about a fifth of the tokens."""
+    E, H, I, k = 128, 2048, 768, 8
+    q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=50 + T)
+    rng = np.random.default_rng(60 + T)
+    h = orc.gen_normal_bf16(rng, (T, H), 2.0)
+    o = orc.gen_normal_bf16(rng, (T, H), 0.5)
+    ln = orc.round_bf16((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    wr = orc.gen_normal_bf16(rng, (E, H), 0.02)
+    out = pkg.moe_sublayer_fp8(to_bf16(h, dev), to_bf16(ln, dev), 1e-6, to_bf16(wr, dev), k, q13, s13, q2, s2,
+                               add=to_bf16(o, dev))
+    got = out.float().cpu().numpy()
+    hs = orc.round_bf16(h + o)
+    x = att.rms_norm(hs, ln, 1e-6)
+    lg = orc.router_logits(x, wr)
+    ids, w, _ = orc.topk_from_logits(lg, k)
+    blk = orc.experts_fp8(x, ids, w, q13.view(torch.uint8).cpu().numpy(), s13.cpu().numpy(),
+                          q2.view(torch.uint8).cpu().numpy(), s2.cpu().numpy(), acc=np.float32)
+    ref = orc.round_bf16(hs + blk)
+    srt = np.sort(lg, axis=1)[:, ::-1]
+    gap_ulps = ulps(srt[:, k - 1], srt[:, k])
+    keep = gap_ulps > 1
+    assert keep.sum() >= max(1, T // 2)
+    d = np.abs(got[keep].astype(np.float64) - ref[keep])
+    mean_rel = d.mean() / np.abs(blk[keep]).mean()  # relative to the block's contribution
+    assert d.max() <= 2e-2 * max(1.0, float(np.abs(ref).max()) / 4) and mean_rel <= 1e-2, (d.max(), mean_rel)
