@@ -128,6 +128,30 @@ int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int 
                          void* weights, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * bf16 experts forward (no FP8 requantisation): the reference's default path for bf16
+ * checkpoints, grouped_mm_experts_forward, TF/integrations/moe.py:377-478.  Same arguments as
+ * moe_mi355x_experts_fp8 with bf16 weights and no scales:
+ *   w13 bf16 [E, 2I, H] (gate rows [0,I), up rows [I,2I)),  w2 bf16 [E, H, I].
+ * Each grouped GEMM returns bf16 (fp32 accumulation), silu(gate) * up in bf16, bf16 routing-weight
+ * product, fp32 slot-order sum, bf16 out.  Constraints: H % 128 == 0, I % 128 == 0, H, I <= 8192.
+ */
+size_t moe_mi355x_experts_bf16_workspace_bytes(int T, int H, int I, int E, int k);
+int moe_mi355x_experts_bf16(const void* x, const void* ids, int id_bytes, const void* weights,
+                            int T, int H, int I, int E, int k, const void* w13, const void* w2,
+                            void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Whole MoE block with bf16 experts: router + moe_mi355x_experts_bf16.
+ * Replaces Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281, as
+ * the reference runs it on a bf16 checkpoint (torch_backend.py:38-40).
+ * logits / ids / weights may be NULL when the caller does not need them.
+ */
+size_t moe_mi355x_block_bf16_workspace_bytes(int T, int H, int I, int E, int k);
+int moe_mi355x_block_bf16(const void* x, const void* w_router, int T, int H, int I, int E, int k,
+                          int renorm, const void* w13, const void* w2, void* out, void* logits, void* ids,
+                          int id_bytes, void* weights, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * moe_mi355x_block_fp8 without a workspace argument and without any allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Its scratch is a fixed device array inside the library,
@@ -145,13 +169,14 @@ int moe_mi355x_block_fp8_noalloc(const void* x, const void* w_router, int T, int
 
 /*
  * Which of the block path's batch-size-dependent launch choices can change its output bits
- * (the router GEMM's K chunks and kernel, the expert GEMMs' tile height): two batch sizes with
- * the same key compute every token's row the same way.  0 for unsupported shapes.  A query
+ * (the router GEMM's K chunks and kernel, the expert GEMMs' tile height), for the FP8 block
+ * (fp8 != 0) or the bf16 block: two batch sizes with the same key compute every token's row the
+ * same way.  0 for unsupported shapes.  A query
  * (host only): a caller that pads batches up to a captured size (a HIP graph per batch bucket)
  * splits its buckets where the key changes, so that a padded batch reproduces the unpadded one
  * bit for bit.  No counterpart in the reference (its eager forward has no buckets).
  */
-long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k);
+long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k, int fp8);
 
 /*
  * Paged GQA decode attention, one new token per sequence (the attention of a decode step of

@@ -29,8 +29,10 @@ from .experts import (  # noqa: F401
 )
 from .kernels import (  # noqa: F401
     align,
+    experts_bf16,
     experts_fp8,
     kv_append,
+    moe_block_bf16,
     moe_block_fp8,
     moe_sublayer_fp8,
     paged_attention_decode,

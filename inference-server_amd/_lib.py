@@ -36,10 +36,16 @@ SIGNATURES = {
     "moe_mi355x_block_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_block_fp8": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_size, _vp]),
+    "moe_mi355x_experts_bf16_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "moe_mi355x_experts_bf16": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                         _vp, _vp, _c_size, _vp]),
+    "moe_mi355x_block_bf16_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "moe_mi355x_block_bf16": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
+                                       _vp, _c_int, _vp, _vp, _c_size, _vp]),
     "moe_mi355x_block_fp8_noalloc_scratch_bytes": (_c_size, []),
     "moe_mi355x_block_fp8_noalloc": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                               _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp]),
-    "moe_mi355x_block_numerics_key": (ctypes.c_longlong, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "moe_mi355x_block_numerics_key": (ctypes.c_longlong, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_paged_attn_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "moe_mi355x_paged_attn_decode": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                               _c_int, _c_int, ctypes.c_float, _vp, _vp, _c_size, _vp]),

@@ -106,6 +106,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   *(uint4*)(out + (long)t * H + c8 * 8) = o;
 }
 
+}  // namespace
+
+// out = bf16(sum_j pairs[t*k + j]) in slot order (+ residual), see combine_kernel.
+int moe_launch_combine(const uint16_t* pairs, const void* ids, int id_bytes, const uint16_t* wts, int T, int k, int H,
+                       int E, const uint16_t* residual, uint16_t* out, hipStream_t s) {
+  const long threads = (long)T * (H / 8);
+  MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, pairs, ids,
+             id_bytes, wts, T, k, H, E, residual, out);
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+namespace {
+
 struct ExpertsWs {
   uint8_t* xq;
   float* sx;
@@ -188,13 +202,8 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
                                 (const uint16_t*)residual);
   if (rc) return rc;
   if (fused_combine) return MOE_OK;
-  const long threads = (long)T * (H / 8);
-  MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                     (const uint16_t*)w.pairs, ids, id_bytes,
-                     w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H, E, (const uint16_t*)residual,
-                     (uint16_t*)out);
-  MOE_CHECK_LAUNCH();
-  return MOE_OK;
+  return moe_launch_combine(w.pairs, ids, id_bytes, w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H,
+                            E, (const uint16_t*)residual, (uint16_t*)out, s);
 }
 
 bool experts_ptrs_ok(const void* x, const void* ids, const void* weights, const void* w13, const float* s13,
@@ -318,11 +327,13 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
 }
 }  // namespace
 
-int moe_route_numerics_key(int T, int H, int E);
+int moe_route_numerics_key(int T, int H, int E, bool quant);
+int moe_bf16_block_m(int S, int E);
 
-extern "C" long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k) {
+extern "C" long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k, int fp8) {
   if (!experts_args_ok(T, H, I, E, k, 4) || T == 0) return 0;
-  return ((long long)moe_route_numerics_key(T, H, E) << 16) | moe_gemm_block_m(T * k, E, H, I);
+  const int bm = fp8 ? moe_gemm_block_m(T * k, E, H, I) : moe_bf16_block_m(T * k, E);
+  return ((long long)moe_route_numerics_key(T, H, E, fp8 != 0) << 16) | bm;
 }
 
 extern "C" int moe_mi355x_block_fp8(const void* x, const void* w_router, int T, int H, int I, int E, int k,

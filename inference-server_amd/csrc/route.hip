@@ -514,11 +514,11 @@ extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E) {
 
 // What of the block path's routing depends on the batch size and can change the bits of the
 // logits: the GEMM kernel (tiled or not) and the K chunks whose fp32 partials are summed.
-int moe_route_numerics_key(int T, int H, int E) {
+int moe_route_numerics_key(int T, int H, int E, bool quant) {
   if (T <= 0 || H <= 0 || E <= 0) return 0;
   const int ks = route_ksplit(T, H, E);
   const bool tiled = route_tiled(T, H);
-  const int kchunk = route_kchunk(H, ks, true);
+  const int kchunk = route_kchunk(H, ks, quant || tiled);
   return (tiled ? 1 << 16 : 0) | kchunk;
 }
 

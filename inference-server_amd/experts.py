@@ -62,16 +62,41 @@ def mi355x_fp8_experts_forward(self: nn.Module, hidden_states: torch.Tensor, top
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
 
+def mi355x_bf16_experts_forward(self: nn.Module, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                                top_k_weights: torch.Tensor) -> torch.Tensor:
+    """Experts forward over bf16 ``gate_up_proj`` [E,2I,H] / ``down_proj`` [E,H,I]
+    (``grouped_mm_experts_forward``, TF/integrations/moe.py:377-478), the reference's path for its
+    default bf16 checkpoints.  Raises ``NotImplementedError`` for layouts it does not cover."""
+    if not getattr(self, "has_gate", True):
+        raise NotImplementedError("the mi355x experts implementation requires gated (gate_up) experts")
+    if getattr(self, "has_bias", False):
+        raise NotImplementedError("the mi355x experts implementation does not support expert biases")
+    if getattr(self, "is_transposed", False):
+        raise NotImplementedError("the mi355x experts implementation expects [E, N, K] (non-transposed) weights")
+    if not getattr(self, "is_concatenated", True):
+        raise NotImplementedError("the mi355x experts implementation expects concatenated [gate; up] weights")
+    out_dtype = hidden_states.dtype
+    x = hidden_states if hidden_states.dtype == torch.bfloat16 else hidden_states.to(torch.bfloat16)
+    w = top_k_weights if top_k_weights.dtype == torch.bfloat16 else top_k_weights.to(torch.bfloat16)
+    out = torch.ops.moe_mi355x.moe_bf16(x.contiguous(), top_k_index.contiguous(), w.contiguous(),
+                                        self.gate_up_proj, self.down_proj)
+    return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
+
+
 def register(key: str = IMPLEMENTATION_KEY) -> bool:
-    """Register the experts forward with transformers' FP8 experts interface.
+    """Register the experts forwards with transformers' experts interfaces: the FP8 one in
+    ``FP8ExpertsInterface`` (finegrained_fp8.py:757-768) and the bf16 one in ``ExpertsInterface``
+    (moe.py:481-506), both under ``key``.
 
     Returns False when transformers is not importable (the modules below still work).
     """
     try:
         from transformers.integrations.finegrained_fp8 import FP8ExpertsInterface
+        from transformers.integrations.moe import ExpertsInterface
     except Exception:  # transformers absent or too old
         return False
     FP8ExpertsInterface.register(key, mi355x_fp8_experts_forward)
+    ExpertsInterface.register(key, mi355x_bf16_experts_forward)
     return True
 
 
@@ -113,6 +138,25 @@ class MI355XFp8Experts(nn.Module):
         return mi355x_fp8_experts_forward(self, hidden_states, top_k_index, top_k_weights)
 
 
+class MI355XBf16Experts(nn.Module):
+    """bf16 experts with the transformers parameter names and layout (``gate_up_proj`` [E,2I,H],
+    ``down_proj`` [E,H,I]): the reference's default bf16 checkpoints, run without requantisation."""
+
+    def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int, device=None):
+        super().__init__()
+        self.num_experts = num_experts
+        self.hidden_dim = hidden_dim
+        self.intermediate_dim = intermediate_dim
+        self.has_gate, self.has_bias, self.is_transposed, self.is_concatenated = True, False, False, True
+        E, H, I = num_experts, hidden_dim, intermediate_dim
+        self.gate_up_proj = nn.Parameter(torch.empty(E, 2 * I, H, dtype=torch.bfloat16, device=device),
+                                         requires_grad=False)
+        self.down_proj = nn.Parameter(torch.empty(E, H, I, dtype=torch.bfloat16, device=device), requires_grad=False)
+
+    def forward(self, hidden_states, top_k_index, top_k_weights):
+        return mi355x_bf16_experts_forward(self, hidden_states, top_k_index, top_k_weights)
+
+
 class MI355XTopKRouter(nn.Module):
     """``Qwen3MoeTopKRouter`` (modeling_qwen3_moe.py:249-267): returns (logits, scores, indices)."""
 
@@ -133,51 +177,67 @@ class MI355XTopKRouter(nn.Module):
 
 
 class MI355XSparseMoeBlock(nn.Module):
-    """Drop-in ``Qwen3MoeSparseMoeBlock``: ``forward(hidden_states[B,S,H]) -> [B,S,H]`` (bf16)."""
+    """Drop-in ``Qwen3MoeSparseMoeBlock``: ``forward(hidden_states[B,S,H]) -> [B,S,H]`` (bf16), with
+    FP8 experts (``MI355XFp8Experts``, the default) or bf16 experts (``MI355XBf16Experts``,
+    ``experts_dtype=torch.bfloat16``)."""
 
     def __init__(self, num_experts: int, hidden_dim: int, intermediate_dim: int, top_k: int,
-                 norm_topk_prob: bool = True, device=None):
+                 norm_topk_prob: bool = True, device=None, experts_dtype=torch.float8_e4m3fn):
         super().__init__()
         self.gate = MI355XTopKRouter(num_experts, hidden_dim, top_k, norm_topk_prob, device=device)
-        self.experts = MI355XFp8Experts(num_experts, hidden_dim, intermediate_dim, device=device)
+        if experts_dtype == torch.bfloat16:
+            self.experts = MI355XBf16Experts(num_experts, hidden_dim, intermediate_dim, device=device)
+        elif experts_dtype == torch.float8_e4m3fn:
+            self.experts = MI355XFp8Experts(num_experts, hidden_dim, intermediate_dim, device=device)
+        else:
+            raise ValueError(f"experts_dtype must be torch.float8_e4m3fn or torch.bfloat16, got {experts_dtype}")
+
+    @property
+    def is_fp8(self) -> bool:
+        return isinstance(self.experts, MI355XFp8Experts)
 
     @classmethod
     def from_hf_block(cls, block: nn.Module, norm_topk_prob: bool | None = None,
                       quantize_fp8: bool = False) -> "MI355XSparseMoeBlock":
-        """Build from a ``Qwen3MoeSparseMoeBlock`` whose experts carry ``FP8Experts`` parameters,
-        or, with ``quantize_fp8=True``, from one with bf16 / fp32 experts, quantised here per
-        128x128 block (``Fp8Quantize``, finegrained_fp8.py:903-941).
+        """Build from a ``Qwen3MoeSparseMoeBlock``.
 
-        The reference loads checkpoints in bf16 (torch_backend.py:38-40) and runs bf16 experts;
-        FP8 requantisation changes the block's numerics (dynamic activation quantisation, FP8
-        weights), so it is never done silently: bf16 experts without ``quantize_fp8=True`` raise
-        ``ValueError``."""
+        * experts with ``FP8Experts`` parameters (an FP8 checkpoint) run on the FP8 path;
+        * bf16 / fp32 experts (the reference loads checkpoints in bf16, torch_backend.py:38-40) run
+          on the bf16 path in bf16, with the reference's numerics;
+        * ``quantize_fp8=True`` requantises bf16 / fp32 experts to FP8 per 128x128 block
+          (``Fp8Quantize``, finegrained_fp8.py:903-941) instead: faster, but it changes the block's
+          numerics (FP8 weights, dynamic activation quantisation), so it is never done silently."""
         gate, experts = block.gate, block.experts
-        if experts.gate_up_proj.dtype != torch.float8_e4m3fn and not quantize_fp8:
-            raise ValueError(
-                f"the experts hold {experts.gate_up_proj.dtype} weights; this block computes in FP8 "
-                "(e4m3, 128x128 block scales, dynamic per-token activation quantisation), which changes the "
-                "model's numerics against its bf16 experts: pass quantize_fp8=True to requantise them")
         E, H = gate.weight.shape
         renorm = gate.norm_topk_prob if norm_topk_prob is None else norm_topk_prob
         dev = gate.weight.device
         I = experts.gate_up_proj.shape[1] // 2
-        new = cls(E, H, I, gate.top_k, renorm, device=dev)
-        if experts.gate_up_proj.dtype == torch.float8_e4m3fn:
+        fp8_in = experts.gate_up_proj.dtype == torch.float8_e4m3fn
+        fp8_out = fp8_in or quantize_fp8
+        new = cls(E, H, I, gate.top_k, renorm, device=dev,
+                  experts_dtype=torch.float8_e4m3fn if fp8_out else torch.bfloat16)
+        if fp8_in:
             with torch.no_grad():
                 for name in ("gate_up_proj", "gate_up_proj_scale_inv", "down_proj", "down_proj_scale_inv"):
                     getattr(new.experts, name).copy_(getattr(experts, name))
-        else:
+        elif quantize_fp8:
             new.experts = MI355XFp8Experts.from_bf16(experts.gate_up_proj.detach(), experts.down_proj.detach())
+        else:
+            with torch.no_grad():
+                new.experts.gate_up_proj.copy_(experts.gate_up_proj.to(torch.bfloat16))
+                new.experts.down_proj.copy_(experts.down_proj.to(torch.bfloat16))
         with torch.no_grad():
             new.gate.weight.copy_(gate.weight.to(torch.bfloat16))
         return new
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         e = self.experts
-        return torch.ops.moe_mi355x.moe_block_fp8(hidden_states.contiguous(), self.gate.weight, self.gate.top_k,
-                                                  bool(self.gate.norm_topk_prob), e.gate_up_proj,
-                                                  e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv)
+        x = hidden_states.contiguous()
+        k, renorm = self.gate.top_k, bool(self.gate.norm_topk_prob)
+        if self.is_fp8:
+            return torch.ops.moe_mi355x.moe_block_fp8(x, self.gate.weight, k, renorm, e.gate_up_proj,
+                                                      e.gate_up_proj_scale_inv, e.down_proj, e.down_proj_scale_inv)
+        return torch.ops.moe_mi355x.moe_block_bf16(x, self.gate.weight, k, renorm, e.gate_up_proj, e.down_proj)
 
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256)
@@ -189,7 +249,7 @@ def swap_moe_blocks(model: nn.Module, quantize_fp8: bool = False, graphed: bool 
 
     Intended right after the reference's ``TorchBackend.load_model`` (torch_backend.py:33-53).
     ``quantize_fp8``: requantise bf16 experts to FP8 (see ``MI355XSparseMoeBlock.from_hf_block``;
-    without it bf16 experts raise).  ``graphed``: wrap each block in ``MI355XGraphedMoeBlock``, so
+    without it bf16 experts run on the bf16 path, FP8 checkpoints on the FP8 path).  ``graphed``: wrap each block in ``MI355XGraphedMoeBlock``, so
     that decode batches up to the largest bucket replay a captured HIP graph (the reference's
     decode loop calls the model once per scheduler step, scheduler.py:396-398).
     """
@@ -203,7 +263,7 @@ def swap_moe_blocks(model: nn.Module, quantize_fp8: bool = False, graphed: bool 
     return len(targets)
 
 
-def numerics_buckets(buckets, hidden: int, intermediate: int, num_experts: int, top_k: int) -> tuple:
+def numerics_buckets(buckets, hidden: int, intermediate: int, num_experts: int, top_k: int, fp8: bool = True) -> tuple:
     """``buckets`` plus an edge at every batch size where the block's numerics key changes
     (``moe_mi355x_block_numerics_key``: router K chunks and kernel, expert tile height), so that
     every batch size in (previous bucket, bucket] computes its rows exactly as the bucket does."""
@@ -211,7 +271,7 @@ def numerics_buckets(buckets, hidden: int, intermediate: int, num_experts: int, 
     if not buckets:
         return ()
     lib = _lib.load()
-    keys = [lib.moe_mi355x_block_numerics_key(t, hidden, intermediate, num_experts, top_k)
+    keys = [lib.moe_mi355x_block_numerics_key(t, hidden, intermediate, num_experts, top_k, int(fp8))
             for t in range(1, buckets[-1] + 1)]
     edges = set(buckets)
     edges.update(t for t in range(1, buckets[-1]) if keys[t - 1] != keys[t])
@@ -241,7 +301,7 @@ class MI355XGraphedMoeBlock(nn.Module):
         self.block = block
         self.requested_buckets = tuple(sorted(set(int(b) for b in buckets)))
         self.buckets = numerics_buckets(buckets, block.gate.hidden_dim, block.experts.intermediate_dim,
-                                        block.gate.num_experts, block.gate.top_k)
+                                        block.gate.num_experts, block.gate.top_k, block.is_fp8)
         self._graphs: dict[int, tuple] = {}
 
     # the wrapped block's modules, so that code written for MI355XSparseMoeBlock finds them

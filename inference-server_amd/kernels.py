@@ -259,6 +259,79 @@ def moe_block_fp8(hidden_states, router_weight, top_k, gate_up_proj, gate_up_pro
     return out
 
 
+def _check_bf16_expert_weights(w13, w2):
+    _need(w13, "gate_up_proj", torch.bfloat16, 3)
+    _need(w2, "down_proj", torch.bfloat16, 3)
+    E, I2, H = w13.shape
+    I = I2 // 2
+    if I2 % 2 or I % BLOCK or H % BLOCK:
+        raise ValueError(f"gate_up_proj must be [E, 2I, H] with I, H multiples of {BLOCK}")
+    if tuple(w2.shape) != (E, H, I):
+        raise ValueError(f"down_proj must be [E, H, I] = {(E, H, I)}, got {tuple(w2.shape)}")
+    if H > 8192 or I > 8192 or not 1 <= E <= 256:
+        raise ValueError("supported shapes: H, I <= 8192 and 1 <= E <= 256")
+    return E, H, I
+
+
+def experts_bf16(hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj):
+    """bf16 experts, ``grouped_mm_experts_forward`` (TF/integrations/moe.py:377-478) on bf16
+    weights ``gate_up_proj`` [E,2I,H] and ``down_proj`` [E,H,I].  Returns bf16 [T, H]."""
+    E, H, I = _check_bf16_expert_weights(gate_up_proj, down_proj)
+    _need(hidden_states, "hidden_states", torch.bfloat16, 2)
+    _need(top_k_index, "top_k_index", (torch.int32, torch.int64), 2)
+    _need(top_k_weights, "top_k_weights", torch.bfloat16, 2)
+    T = hidden_states.shape[0]
+    if hidden_states.shape[1] != H:
+        raise ValueError(f"hidden_states must be [T, {H}]")
+    if top_k_index.shape[0] != T or tuple(top_k_weights.shape) != tuple(top_k_index.shape):
+        raise ValueError("top_k_index and top_k_weights must both be [T, k]")
+    k = top_k_index.shape[1]
+    if not 1 <= k <= min(E, 32):
+        raise ValueError("k must be in [1, min(E, 32)]")
+    lib = _lib.load()
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden_states.device)
+    ws = _ws(lib.moe_mi355x_experts_bf16_workspace_bytes(T, H, I, E, k), hidden_states.device)
+    _lib.check(lib.moe_mi355x_experts_bf16(hidden_states.data_ptr(), top_k_index.data_ptr(), _id_bytes(top_k_index),
+                                           top_k_weights.data_ptr(), T, H, I, E, k, gate_up_proj.data_ptr(),
+                                           down_proj.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                           _stream(hidden_states)), "moe_mi355x_experts_bf16")
+    return out
+
+
+def moe_block_bf16(hidden_states, router_weight, top_k, gate_up_proj, down_proj, norm_topk_prob=True,
+                   return_routing=False, index_dtype=torch.int64):
+    """Router + bf16 experts (``Qwen3MoeSparseMoeBlock.forward`` on a bf16 checkpoint,
+    TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281).  hidden_states: [..., H] bf16."""
+    E, H, I = _check_bf16_expert_weights(gate_up_proj, down_proj)
+    _need(router_weight, "router_weight", torch.bfloat16, 2)
+    if tuple(router_weight.shape) != (E, H):
+        raise ValueError(f"router_weight must be [{E}, {H}]")
+    shape = hidden_states.shape
+    x = hidden_states.reshape(-1, H)
+    _need(x, "hidden_states", torch.bfloat16, 2)
+    if not 1 <= top_k <= min(E, 32):
+        raise ValueError("top_k must be in [1, min(E, 32)]")
+    T = x.shape[0]
+    lib = _lib.load()
+    dev = x.device
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    logits = ids = w = None
+    if return_routing:
+        logits = torch.empty((T, E), dtype=torch.bfloat16, device=dev)
+        ids = torch.empty((T, top_k), dtype=index_dtype, device=dev)
+        w = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+    ws = _ws(lib.moe_mi355x_block_bf16_workspace_bytes(T, H, I, E, top_k), dev)
+    _lib.check(lib.moe_mi355x_block_bf16(
+        x.data_ptr(), router_weight.data_ptr(), T, H, I, E, top_k, int(norm_topk_prob), gate_up_proj.data_ptr(),
+        down_proj.data_ptr(), out.data_ptr(), logits.data_ptr() if logits is not None else None,
+        ids.data_ptr() if ids is not None else None, _id_bytes(ids) if ids is not None else 4,
+        w.data_ptr() if w is not None else None, ws.data_ptr(), ws.numel(), _stream(x)), "moe_mi355x_block_bf16")
+    out = out.reshape(shape)
+    if return_routing:
+        return out, (logits, w, ids)
+    return out
+
+
 # ---------------------------------------------------------------------------
 # paged decode attention
 # ---------------------------------------------------------------------------

@@ -16,6 +16,10 @@ shapes and dtypes from input metadata alone, so the operators trace under FakeTe
       fp8_grouped_mm_experts_forward, TF/integrations/finegrained_fp8.py:498-589
   moe_block_fp8(x bf16[...,H], w_router, k, renorm, w13, s13, w2, s2) -> bf16[...,H]
       Qwen3MoeSparseMoeBlock.forward, modeling_qwen3_moe.py:276-281
+  moe_bf16(x bf16[T,H], ids, weights, w13 bf16[E,2I,H], w2 bf16[E,H,I]) -> bf16[T,H]
+      grouped_mm_experts_forward on bf16 weights, TF/integrations/moe.py:377-478
+  moe_block_bf16(x bf16[...,H], w_router, k, renorm, w13, w2) -> bf16[...,H]
+      the block on a bf16 checkpoint
 
 Weights: w13 e4m3fn [E,2I,H] with s13 fp32 [E,2I/128,H/128]; w2 e4m3fn [E,H,I] with s2 fp32
 [E,H/128,I/128].  The operators are registered when the package is imported (once per process).
@@ -86,9 +90,27 @@ def _define() -> None:
     def _(x, w_router, k, renorm, w13, s13, w2, s2):
         return x.new_empty(x.shape, dtype=torch.bfloat16)
 
+    @torch.library.custom_op(lib + "moe_bf16", mutates_args=())
+    def moe_bf16(x: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor, w13: torch.Tensor,
+                 w2: torch.Tensor) -> torch.Tensor:
+        return kernels.experts_bf16(x, ids, weights, w13, w2)
+
+    @moe_bf16.register_fake
+    def _(x, ids, weights, w13, w2):
+        return x.new_empty((x.shape[0], w2.shape[1]), dtype=torch.bfloat16)
+
+    @torch.library.custom_op(lib + "moe_block_bf16", mutates_args=())
+    def moe_block_bf16(x: torch.Tensor, w_router: torch.Tensor, k: int, renorm: bool, w13: torch.Tensor,
+                       w2: torch.Tensor) -> torch.Tensor:
+        return kernels.moe_block_bf16(x, w_router, k, w13, w2, norm_topk_prob=renorm)
+
+    @moe_block_bf16.register_fake
+    def _(x, w_router, k, renorm, w13, w2):
+        return x.new_empty(x.shape, dtype=torch.bfloat16)
+
 
 def registered() -> bool:
-    return hasattr(torch.ops, NAMESPACE) and hasattr(getattr(torch.ops, NAMESPACE), "moe_block_fp8")
+    return hasattr(torch.ops, NAMESPACE) and hasattr(getattr(torch.ops, NAMESPACE), "moe_block_bf16")
 
 
 def register() -> None:

@@ -38,7 +38,7 @@ pytestmark = pytest.mark.gpu
 
 def block_m_of(pkg, T, H, I, E, k):
     """Tile height the library picks for T tokens (low 16 bits of the numerics key)."""
-    return int(pkg._lib.load().moe_mi355x_block_numerics_key(T, H, I, E, k)) & 0xFFFF
+    return int(pkg._lib.load().moe_mi355x_block_numerics_key(T, H, I, E, k, 1)) & 0xFFFF
 
 
 def tile_stratified_tokens(ids, E, block_m, rng):

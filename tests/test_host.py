@@ -111,22 +111,24 @@ def test_align_max_tiles_matches_library(pkg):
                 assert pkg.torch_ops.align_max_tiles(S, E, bm) == max(lib.moe_mi355x_align_max_tiles(S, E, bm), 1)
 
 
-def test_bf16_experts_need_explicit_fp8_opt_in(pkg):
-    """The reference runs bf16 experts (torch_backend.py:38-40); turning them into FP8 changes the
-    numerics, so the swap refuses bf16 experts unless quantize_fp8=True is passed."""
+def test_bf16_experts_stay_bf16_unless_fp8_is_requested(pkg):
+    """The reference runs bf16 experts (torch_backend.py:38-40): the swap keeps them bf16 (the
+    bf16 path) unless quantize_fp8=True asks for the FP8 requantisation."""
     pytest.importorskip("transformers")
     from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
     from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeForCausalLM
 
-    cfg = Qwen3MoeConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=1,
+    cfg = Qwen3MoeConfig(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=2,
                          num_attention_heads=2, num_key_value_heads=1, head_dim=128, num_experts=8,
                          num_experts_per_tok=2, moe_intermediate_size=128, norm_topk_prob=True)
     with torch.device("meta"):
         model = Qwen3MoeForCausalLM(cfg).to(torch.bfloat16)
-    with pytest.raises(ValueError, match="quantize_fp8=True"):
-        pkg.swap_moe_blocks(model)
-    with pytest.raises(ValueError, match="quantize_fp8=True"):
-        pkg.MI355XSparseMoeBlock.from_hf_block(model.model.layers[0].mlp)
+    assert pkg.swap_moe_blocks(model) == 2
+    for layer in model.model.layers:
+        assert isinstance(layer.mlp, pkg.MI355XSparseMoeBlock) and not layer.mlp.is_fp8
+        assert isinstance(layer.mlp.experts, pkg.experts.MI355XBf16Experts)
+        assert layer.mlp.experts.gate_up_proj.dtype == torch.bfloat16
+        assert tuple(layer.mlp.experts.gate_up_proj.shape) == (8, 256, 256)
 
 
 @pytest.mark.parametrize("H,I,E,k", [(2048, 768, 128, 8), (2048, 768, 100, 6), (4096, 1536, 128, 8),
@@ -139,10 +141,10 @@ def test_numerics_buckets_split_at_key_changes(pkg, H, I, E, k):
     assert set(pkg.experts.DEFAULT_BUCKETS) <= set(buckets)
     prev = 0
     for b in buckets:
-        kb = lib.moe_mi355x_block_numerics_key(b, H, I, E, k)
+        kb = lib.moe_mi355x_block_numerics_key(b, H, I, E, k, 1)
         assert kb != 0
         for t in range(prev + 1, b + 1):
-            assert lib.moe_mi355x_block_numerics_key(t, H, I, E, k) == kb, (t, b)
+            assert lib.moe_mi355x_block_numerics_key(t, H, I, E, k, 1) == kb, (t, b)
         prev = b
     # the tile height changes at S = 8 E and S = 16 E: both are bucket edges
     for edge in (8 * E // k, 16 * E // k):
