@@ -94,11 +94,11 @@ S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 # HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy):
 #   decode 64:            rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} ... -- python3 bench.py --no-sweep --no-cpu
-#                         --steps 10 --warmup 2 --copy-probe           -> 195,244 / 768 KiB
+#                         --steps 10 --warmup 2 --copy-probe           -> 195,732 / 1,381 KiB
 #   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
 #                         --copy-probe                                 -> 291,674 / 25,447 KiB
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): 195244 * 1024 * 2 + 768 * 1024,
+    ("qwen3-30b-a3b", 64): 195732 * 1024 * 2 + 1381 * 1024,
     ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
 }
 
