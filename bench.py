@@ -191,6 +191,8 @@ def run_config(pkg, torch, layer, T, steps, warmup, router, xs):
     torch.cuda.synchronize()
     slots = {}
     for slot in range(N_SLOTS):
+        if not lib.moe_mi355x_profile_slot_name(slot):
+            continue
         n, tot = ctypes.c_int(0), ctypes.c_double(0.0)
         pkg._lib.check(lib.moe_mi355x_profile_read(slot, ctypes.byref(n), ctypes.byref(tot)), "profile_read")
         if n.value:

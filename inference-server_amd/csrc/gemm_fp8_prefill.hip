@@ -10,21 +10,20 @@
 //   down:    256 output columns; epilogue bf16(z) * routing weight, stored at the pair's
 //            original row t*k+j.
 //
-// Workgroup: 4 waves, one per SIMD, in a 2x2 grid; a wave owns 64 rows x 128 weight rows
-// = 4 x 8 v_mfma_f32_16x16x128_f8f6f4 tiles per K block, each folded into the fp32
-// accumulator with the (activation row scale x weight tile scale) product.  The 64x128
-// wave tile reads 24 KB of LDS per 32 MFMAs (0.75 KB per MFMA).
+// Workgroup: 8 waves, two per SIMD, in a 2 (rows) x 4 (weight rows) grid; a wave owns 64
+// rows x 64 weight rows = 4 x 4 v_mfma_f32_16x16x128_f8f6f4 tiles per K block, each folded
+// into the fp32 accumulator with the (activation row scale x weight tile scale) product.
 //
 // Pipeline, per K block kb: one barrier, after which (1) the DMA of K block kb+3 is issued
 // into the LDS stage kb just vacated, (2) the fragments of K block kb+1 are read from LDS
-// into the second register set, (3) the 32 MFMAs of K block kb run on the first set, with
+// into the second register set, (3) the 16 MFMAs of K block kb run on the first set, with
 // the scale FMAs of each MFMA trailing it.  LDS reads, DMA and MFMA/VALU of one wave thus
 // overlap instead of alternating across barriers.
 //
 // Operands are staged through a ring of three 48.5 KB LDS stages (A 16 KB + B 32 KB +
 // 512 B of activation scales) filled by global->LDS DMA without touching VGPRs.  LDS rows
-// are 128 bytes; 16-byte chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), so the
-// lanes that share an LDS cycle in a ds_read_b128 of an MFMA fragment hit distinct banks.
+// are 128 bytes, XOR-swizzled in 16-byte chunks (swz_key below) so that the lanes sharing an
+// LDS cycle in a ds_read_b128 of an MFMA fragment hit distinct banks.
 //
 // Persistent grid: one workgroup per CU (the LDS footprint allows one).  Work items
 // (tile, column block) are handed out so that the workgroups resident on one XCD
