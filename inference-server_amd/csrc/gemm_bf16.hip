@@ -189,18 +189,29 @@ int launch_bf16_gemm(const Bf16GemmArgs& a, int max_tiles, hipStream_t s) {
 
 }  // namespace
 
-// Tile height for the bf16 path: 16- and 32-row tiles as the FP8 decode GEMMs, 64 above.
-int moe_bf16_block_m(int S, int E) {
+bool moe_prefill_bf16_ok(int H, int I, long max_rows);
+int moe_launch_grouped_gemms_prefill_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2,
+                                          const int32_t* perm, const int32_t* tiles, const int32_t* n_tiles,
+                                          int max_tiles, uint16_t* h, uint16_t* pairs, int H, int I, int k,
+                                          hipStream_t s);
+extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m);
+
+// Tile height for the bf16 path: 16- and 32-row tiles as the FP8 decode GEMMs; above, the
+// 128-row LDS-tiled prefill kernel where the shape allows it (64-row tiles otherwise).
+int moe_bf16_block_m(int S, int E, int H, int I) {
   if (S <= 8 * E) return 16;
   if (S <= 16 * E) return 32;
-  return 64;
+  return moe_prefill_bf16_ok(H, I, 128L * moe_mi355x_align_max_tiles(S, E, 128)) ? 128 : 64;
 }
 
-// gate_up (fused SiLU*up, bf16 h) then down (weighted pair rows), bf16 weights.
+// gate_up (fused SiLU*up, bf16 h) then down (weighted pair rows; on 128-row tiles bf16(z) rows
+// that the combine weights), bf16 weights.
 int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2, const int32_t* perm,
                                   const int32_t* tiles, const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w,
                                   uint16_t* h, uint16_t* pairs, int S, int H, int I, int k, int block_m,
                                   hipStream_t s) {
+  if (block_m == 128)
+    return moe_launch_grouped_gemms_prefill_bf16(x, w13, w2, perm, tiles, n_tiles, max_tiles, h, pairs, H, I, k, s);
   Bf16GemmArgs g1{x, w13, perm, tiles, n_tiles, nullptr, h, H, I, k};
   int rc;
   if (block_m == 16)

@@ -57,7 +57,8 @@ struct PrefillArgs {
   uint16_t* pairs;         // down: output [S, N] by flat pair
   uint8_t* hq;             // gate_up: e4m3 intermediate [S, N]
   float* sh;               // gate_up: its scales [S, N/128]
-  int K;                   // reduction length
+  uint16_t* h;             // bf16 weights, gate_up: the bf16 intermediate [S, N]
+  int K;                   // reduction length (elements)
   int N;                   // gate_up: I; down: H
   int topk;
   int n_nblk;              // column blocks per tile: gate_up I/128, down H/256
@@ -141,7 +142,17 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs& p, int item) {
   return {ti.x, ti.y, ti.z, item - tile * p.n_nblk};
 }
 
-template <int MODE>
+// Splits one lane's 32-byte fragment of a 128-byte K block into the two 16-byte operands of the
+// bf16 MFMAs (chunks 2 g and 2 g + 1 of the row for lane group g).
+__device__ __forceinline__ v8bf frag_half(const v8i& f, int h) {
+  return __builtin_bit_cast(v8bf, make_uint4(f[4 * h], f[4 * h + 1], f[4 * h + 2], f[4 * h + 3]));
+}
+
+// BF: bf16 activations and weights (a bf16 checkpoint).  A K block is then 64 elements, still 128
+// bytes per row, so the LDS layout, the DMA and the fragment reads are the same; each fragment
+// feeds two v_mfma_f32_16x16x32_bf16 (lane group g supplies K chunks 2 g and 2 g + 1, the same
+// K permutation for both operands), which accumulate in fp32 in the MFMA: no scales, no FMAs.
+template <int MODE, bool BF>
 __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(PrefillArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_ab[3][P_STAGE3];
   __shared__ __attribute__((aligned(16))) int s_perm[2][PBM];  // perm rows of the item, by item parity
@@ -153,7 +164,9 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
   const int wm = wave & 1, wn = wave >> 1;  // 2 x 4 waves: rows wm*64, weight-column quarter wn
   const int lr = lane & 15, lg = lane >> 4;
   const int c0 = 2 * lg;
-  const int K = p.K, KB = K / PBK;
+  const int K = BF ? 2 * p.K : p.K;  // bytes per operand row
+  const int KB = K / PBK;              // 128-byte K blocks
+  constexpr int DPS = BF ? P_DMA_A + P_DMA_B : P_DMA_PER_STEP;  // DMA instructions per step and wave
   const int Nw = MODE == PF_GATE_UP ? 2 * p.N : p.N;
   const int nblk128 = Nw / PBK;
   const int n_items = const_ld(p.n_tiles, 0) * p.n_nblk;
@@ -208,7 +221,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     if (lane < 16)                                                                                \
       dma_b32<0>((uint32_t)((it_).row0 + min(r_, (it_).rows - 1)) * 4u, p.perm,                  \
                  lds_perm0 + ((j_) & 1) * (PBM * 4) + 64 * wave);                                 \
-    if (wave < 2 && lane < KB) {                                                                  \
+    if (!BF && wave < 2 && lane < KB) {                                                           \
       const int blk_ = MODE == PF_GATE_UP ? (wave == 0 ? (it_).nb : p.N / PBK + (it_).nb) : 2 * (it_).nb + wave; \
       dma_b32<0>((uint32_t)(((it_).e * nblk128 + blk_) * KB + lane) * 4u, p.sw,                  \
                  lds_swt0 + (((j_) & 1) * 2 + wave) * (kMaxKB * 4));                              \
@@ -238,14 +251,15 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     if constexpr ((d_) < P_DMA_A) dma_b128<(d_) * 8192>(a_voff[d_], ab_, sbw_);                   \
     else if constexpr ((d_) < P_DMA_A + P_DMA_B)                                                  \
       dma_b128<P_A + ((d_) - P_DMA_A) * 8192>(b_voff[(d_) - P_DMA_A], bb_, sbw_);                 \
-    else if (lane < 16) dma_b32<0>(sa_voff, sab_, (sbw_) - 1024 * wave + P_STAGE + 64 * wave);    \
+    else if (!BF && lane < 16) dma_b32<0>(sa_voff, sab_, (sbw_) - 1024 * wave + P_STAGE + 64 * wave); \
   } while (0)
 
   // weight tile scales of K block kb_ of item j_ for this wave: gate_up (gate, up); down the
   // 128-row half of the wave's columns
 #define PF_SW(SW_, j_, kb_)                                                                       \
   do {                                                                                            \
-    if constexpr (MODE == PF_GATE_UP) {                                                           \
+    if constexpr (BF) {                                                                           \
+    } else if constexpr (MODE == PF_GATE_UP) {                                                    \
       SW_[0] = s_swt[(j_) & 1][0][kb_];                                                           \
       SW_[1] = s_swt[(j_) & 1][1][kb_];                                                           \
     } else {                                                                                      \
@@ -262,7 +276,9 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     const float* sS_ = (const float*)(sA_ + P_STAGE);                                             \
     _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) A_[mi] = lds_frag(sA_, wm * 64 + mi * 16 + lr, c0); \
     _Pragma("unroll") for (int ni = 0; ni < 4; ++ni) B_[ni] = lds_frag(sB_, PF_BROW(ni), c0);     \
-    _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) SV_[mi] = sS_[wm * 64 + mi * 16 + lr];       \
+    if constexpr (!BF) {                                                                          \
+      _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) SV_[mi] = sS_[wm * 64 + mi * 16 + lr];     \
+    }                                                                                             \
   } while (0)
 
   // One step's 16 MFMAs (A fragments AC, B fragments B, scales SC/WC; MFMA order ni-major)
@@ -336,6 +352,34 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     }                                                                                             \
   } while (0)
 
+  // bf16: 32 MFMAs per step, for each weight fragment ni its low halves (mi = 0..3) then its
+  // high halves, so that an accumulator's two MFMAs are four MFMAs apart; the next step's A
+  // fragments are read in slots 0-7 and each B fragment is reloaded in place after its last MFMA
+#define PF_STEP_BODY_BF(AC, AN, B, st_, ab_, bb_, sab_, sbw_)                                     \
+  do {                                                                                            \
+    const uint8_t* sA_ = s_ab[st_];                                                               \
+    const uint8_t* sB_ = sA_ + P_A;                                                               \
+    _Pragma("unroll") for (int it = 0; it < 34; ++it) {                                           \
+      if (it < 32) {                                                                              \
+        const int ni = it >> 3, hh = (it >> 2) & 1, mi = it & 3;                                  \
+        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag_half(B[ni], hh), frag_half(AC[mi], hh), \
+                                                              acc[mi][ni], 0, 0, 0);             \
+      }                                                                                           \
+      if (it < 8) PF_RD_A(AN, it >> 1, it & 1);                                                   \
+      if (it == 8 || it == 9) PF_RD_B(B, 0, it - 8);                                              \
+      if (it == 16 || it == 17) PF_RD_B(B, 1, it - 16);                                           \
+      if (it == 24 || it == 25) PF_RD_B(B, 2, it - 24);                                           \
+      if (it == 32 || it == 33) PF_RD_B(B, 3, it - 32);                                           \
+      if (it == 1) PF_DMA_ONE(0, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 3) PF_DMA_ONE(1, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 5) PF_DMA_ONE(2, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 7) PF_DMA_ONE(3, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 9) PF_DMA_ONE(4, ab_, bb_, sab_, sbw_);                                           \
+      if (it == 11) PF_DMA_ONE(5, ab_, bb_, sab_, sbw_);                                          \
+      __builtin_amdgcn_sched_barrier(0);                                                          \
+    }                                                                                             \
+  } while (0)
+
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
   v4f acc[4][4];
 #pragma unroll
@@ -368,7 +412,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     PF_DMA_ONE(5, ab_, bb_, sab_, sbw_);
     PF_DMA_ONE(6, ab_, bb_, sab_, sbw_);
   }
-  wait_vm<2 * P_DMA_PER_STEP>();
+  wait_vm<2 * DPS>();
   lds_wait_barrier();
   PF_READ(a0, bf, sv0, 0);
   PF_SW(sw_0, 0, 0);
@@ -385,7 +429,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
 #define PF_STEP(AC, AN, SC, SN, WC, WN)                                                           \
   do {                                                                                            \
     if (s + 2 < S_tot)                                                                            \
-      wait_vm<P_DMA_PER_STEP>();                                                                  \
+      wait_vm<DPS>();                                                                             \
     else                                                                                          \
       wait_vm<0>();                                                                               \
     lds_wait_barrier();                                                                           \
@@ -412,7 +456,10 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     const int last_ = kb == KB - 1;                                                               \
     const int st1_ = st == 2 ? 0 : st + 1;                                                        \
     /* fragments of step s+1 (past the last step: a harmless read of a stale stage) */           \
-    PF_STEP_BODY(AC, AN, bf, SC, SN, WC, WN, st1_, j + last_, last_ ? 0 : kb + 1, ab_, bb_, sab_, sbw_); \
+    if constexpr (BF)                                                                             \
+      PF_STEP_BODY_BF(AC, AN, bf, st1_, ab_, bb_, sab_, sbw_);                                    \
+    else                                                                                          \
+      PF_STEP_BODY(AC, AN, bf, SC, SN, WC, WN, st1_, j + last_, last_ ? 0 : kb + 1, ab_, bb_, sab_, sbw_); \
     if (last_) {                                                                                  \
       pf_epilogue(j);                                                                             \
       _Pragma("unroll") for (int mi = 0; mi < 4; ++mi)                                            \
@@ -431,7 +478,24 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
   // r = wm*64 + mi*16 + lr, the columns 16 ni + 4 lg + q of this wave's weight rows
   auto pf_epilogue = [&](int jj) __attribute__((always_inline)) {
     const int row0 = it_c.row0, rows = it_c.rows, nb = it_c.nb;
-    if constexpr (MODE == PF_GATE_UP) {
+    if constexpr (MODE == PF_GATE_UP && BF) {
+      // h = bf16(bf16(silu(bf16 g)) * bf16 u) in bf16, four consecutive h columns per lane and row
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int r = wm * 64 + mi * 16 + lr;
+        if (r >= rows) continue;
+        uint16_t* dst = p.h + (long)(row0 + r) * p.N + nb * 128 + wn * 32 + 4 * lg;
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          uint2 v;
+          v.x = (uint32_t)f32_to_bf16(silu_mul_bf16(acc[mi][ni][0], acc[mi][ni + 2][0])) |
+                ((uint32_t)f32_to_bf16(silu_mul_bf16(acc[mi][ni][1], acc[mi][ni + 2][1])) << 16);
+          v.y = (uint32_t)f32_to_bf16(silu_mul_bf16(acc[mi][ni][2], acc[mi][ni + 2][2])) |
+                ((uint32_t)f32_to_bf16(silu_mul_bf16(acc[mi][ni][3], acc[mi][ni + 2][3])) << 16);
+          *(uint2*)(dst + ni * 16) = v;
+        }
+      }
+    } else if constexpr (MODE == PF_GATE_UP) {
       // h = bf16(bf16(silu(bf16 g)) * bf16 u): gate frags 0, 1 pair with up frags 2, 3, so
       // this wave holds h columns wn*32 + 16 ni + 4 lg + q
       float rmax[4];
@@ -503,6 +567,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
   }
 #undef PF_STEP
 #undef PF_STEP_BODY
+#undef PF_STEP_BODY_BF
 #undef PF_RD_A
 #undef PF_RD_B
 #undef PF_READ
@@ -525,14 +590,14 @@ int device_cu_count() {
   return cus;
 }
 
-template <int MODE>
+template <int MODE, bool BF = false>
 int launch_prefill(const PrefillArgs& a, int max_tiles, hipStream_t s) {
   const long max_items = (long)max_tiles * a.n_nblk;
   long g = device_cu_count();
   if (g > max_items) g = max_items;
   g = (g + 7) / 8 * 8;
   if (g < 8) g = 8;
-  MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, grouped_gemm_fp8_prefill_kernel<MODE>,
+  MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_prefill_kernel<MODE, BF>),
              dim3((unsigned)g), dim3(P_THREADS), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -551,9 +616,31 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
   if (max_rows * (H > I ? H : I) >= (1L << 32)) return MOE_ERR_INVALID_ARG;
   // the cross-item DMA pipeline needs at least 4 K blocks per GEMM
   if (H / PBK < 4 || I / PBK < 4 || H % PBN != 0) return MOE_ERR_INVALID_ARG;
-  PrefillArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, nullptr, hq, sh, H, I, k, I / PBK};
+  PrefillArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, nullptr, hq, sh, nullptr, H, I, k, I / PBK};
   int rc = launch_prefill<PF_GATE_UP>(g1, max_tiles, s);
   if (rc) return rc;
-  PrefillArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, nullptr, nullptr, I, H, k, H / PBN};
+  PrefillArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, nullptr, nullptr, nullptr, I, H, k, H / PBN};
   return launch_prefill<PF_DOWN>(g2, max_tiles, s);
+}
+
+// Whether bf16 experts of this shape can take the 128-row tiles (bf16 K blocks are 64 deep).
+bool moe_prefill_bf16_ok(int H, int I, long max_rows) {
+  return H % PBN == 0 && H / 64 >= 4 && I / 64 >= 4 && I % MOE_GROUP == 0 &&
+         max_rows * 2 * (H > I ? H : I) < (1L << 32);
+}
+
+// The same pair of GEMMs for bf16 weights: gate_up writes bf16 h [S, I], down bf16(z) pair rows
+// (the combine applies the routing weight).
+int moe_launch_grouped_gemms_prefill_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2,
+                                          const int32_t* perm, const int32_t* tiles, const int32_t* n_tiles,
+                                          int max_tiles, uint16_t* h, uint16_t* pairs, int H, int I, int k,
+                                          hipStream_t s) {
+  if (!moe_prefill_bf16_ok(H, I, (long)max_tiles * PBM)) return MOE_ERR_INVALID_ARG;
+  PrefillArgs g1{(const uint8_t*)x, nullptr, (const uint8_t*)w13, nullptr, perm, tiles, n_tiles, nullptr, nullptr,
+                 nullptr, nullptr, h, H, I, k, I / PBK};
+  int rc = launch_prefill<PF_GATE_UP, true>(g1, max_tiles, s);
+  if (rc) return rc;
+  PrefillArgs g2{(const uint8_t*)h, nullptr, (const uint8_t*)w2, nullptr, perm, tiles, n_tiles, nullptr, pairs,
+                 nullptr, nullptr, nullptr, I, H, k, H / PBN};
+  return launch_prefill<PF_DOWN, true>(g2, max_tiles, s);
 }

@@ -328,11 +328,11 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
 }  // namespace
 
 int moe_route_numerics_key(int T, int H, int E, bool quant);
-int moe_bf16_block_m(int S, int E);
+int moe_bf16_block_m(int S, int E, int H, int I);
 
 extern "C" long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k, int fp8) {
   if (!experts_args_ok(T, H, I, E, k, 4) || T == 0) return 0;
-  const int bm = fp8 ? moe_gemm_block_m(T * k, E, H, I) : moe_bf16_block_m(T * k, E);
+  const int bm = fp8 ? moe_gemm_block_m(T * k, E, H, I) : moe_bf16_block_m(T * k, E, H, I);
   return ((long long)moe_route_numerics_key(T, H, E, fp8 != 0) << 16) | bm;
 }
 

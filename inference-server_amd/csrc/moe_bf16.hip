@@ -7,7 +7,7 @@
 // :509-520), and Qwen3MoeSparseMoeBlock.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:276-281.
 #include "common.h"
 
-int moe_bf16_block_m(int S, int E);
+int moe_bf16_block_m(int S, int E, int H, int I);
 int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2, const int32_t* perm,
                                   const int32_t* tiles, const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w,
                                   uint16_t* h, uint16_t* pairs, int S, int H, int I, int k, int block_m,
@@ -47,7 +47,7 @@ struct Bf16Ws {
 Bf16Ws carve_bf16(void* base, int T, int H, int I, int E, int k) {
   Bf16Ws w{};
   const int S = T * k;
-  w.block_m = moe_bf16_block_m(S, E);
+  w.block_m = moe_bf16_block_m(S, E, H, I);
   w.max_tiles = moe_mi355x_align_max_tiles(S, E, w.block_m);
   WsCarver c(base);
   w.perm = c.take<int32_t>(S);
@@ -76,7 +76,9 @@ int bf16_experts_after_align(const void* x, const void* ids, int id_bytes, const
                                          w.tiles, w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.pairs,
                                          T * k, H, I, k, w.block_m, s);
   if (rc) return rc;
-  return moe_launch_combine(w.pairs, ids, id_bytes, nullptr, T, k, H, E, nullptr, (uint16_t*)out, s);
+  // the 128-row tiles leave the routing-weight product to the combine
+  return moe_launch_combine(w.pairs, ids, id_bytes, w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k,
+                            H, E, nullptr, (uint16_t*)out, s);
 }
 
 struct Bf16BlockWs {

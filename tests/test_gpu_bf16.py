@@ -7,7 +7,9 @@ GPU, through the C ABI.
   ulps of the output scale (the
   bf16 MFMA accumulates exactly in fp32; only the order of fp32 additions differs).
 * the block (router + bf16 experts) against the oracle's bf16 grouped chain on the kernel's
-  routing, at every tile height (16-, 32- and 64-row tiles);
+  routing, at every tile height (16-, 32-, 64- and the LDS-tiled 128-row tiles);
+* the 4096-token Zipf-skewed prefill chunk (C3's routing) on bf16 experts, one token of every
+  128-row tile checked;
 * a tiny Qwen3-MoE LM swapped with bf16 blocks, and one dispatching its bf16 experts through
   transformers' ``ExpertsInterface`` under the ``"mi355x"`` key, against transformers' own
   ``grouped_mm`` experts on the same GPU.
@@ -50,10 +52,21 @@ def test_bf16_experts_reproduce_transformers_golden(pkg, dev, case):
     assert d.max() <= 2.0 ** -8 * max(float(np.abs(ref).max()), 1e-3) * 2, d.max()
 
 
-@pytest.mark.parametrize("T,H,I,E,k", [(1, 2048, 768, 128, 8), (16, 2048, 768, 128, 8), (64, 2048, 768, 128, 8),
-                                       (200, 2048, 768, 128, 8), (600, 2048, 768, 128, 8), (37, 384, 256, 20, 5)])
-def test_bf16_block_matches_oracle(pkg, dev, T, H, I, E, k):
-    """16-row tiles (S <= 8 E), 32-row tiles (S <= 16 E), 64-row tiles above."""
+def bf16_block_m(pkg, T, H, I, E, k):
+    """Tile height of the bf16 path for T tokens (low 16 bits of the numerics key)."""
+    return int(pkg._lib.load().moe_mi355x_block_numerics_key(T, H, I, E, k, 0)) & 0xFFFF
+
+
+@pytest.mark.parametrize("T,H,I,E,k,bm", [(1, 2048, 768, 128, 8, 16), (16, 2048, 768, 128, 8, 16),
+                                          (64, 2048, 768, 128, 8, 16), (200, 2048, 768, 128, 8, 32),
+                                          (600, 2048, 768, 128, 8, 128), (37, 384, 256, 20, 5, 32),
+                                          (100, 384, 256, 8, 2, 64), (257, 1024, 640, 12, 6, 128),
+                                          (600, 4096, 1536, 16, 8, 128), (40, 512, 256, 4, 2, 128)])
+def test_bf16_block_matches_oracle(pkg, dev, T, H, I, E, k, bm):
+    """16-row tiles (S <= 8 E), 32-row tiles (S <= 16 E), above the 128-row LDS-tiled kernel
+    (64-row tiles when H % 256 != 0); 128-row cases at the 30B and 235B widths, with 5 K blocks of
+    128 in the down GEMM's h (I = 640) and with the minimum of 4 bf16 K blocks (I = 256)."""
+    assert bf16_block_m(pkg, T, H, I, E, k) == bm
     rng = np.random.default_rng(400 + T + H)
     x = orc.gen_normal_bf16(rng, (T, H))
     wr = orc.gen_normal_bf16(rng, (E, H), 0.02)
@@ -73,6 +86,31 @@ def test_bf16_block_matches_oracle(pkg, dev, T, H, I, E, k):
     max_abs, mean_rel = errors(got, ref)
     assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
     # the GEMMs accumulate exactly in fp32: nearly every output is the oracle's bf16 value
+    assert (bf16_ulp_diff(got, ref) == 0).mean() >= 0.95
+
+
+def test_bf16_prefill_zipf_every_tile(pkg, dev):
+    """C3's routing (4096 tokens, Zipf-skewed: a few hot experts with many tiles, ragged last
+    tiles) on bf16 30B experts, 128-row tiles; the first, the last and a random row of every tile
+    are checked against the oracle's bf16 chain."""
+    from tests.test_gpu_configs import tile_stratified_tokens
+
+    T, H, I, E, k = 4096, 2048, 768, 128, 8
+    assert bf16_block_m(pkg, T, H, I, E, k) == 128
+    rng = np.random.default_rng(12)
+    x = orc.gen_normal_bf16(rng, (T, H))
+    lg = orc.gen_normal_bf16(rng, (T, E)) + orc.zipf_bias(E, 1.1, beta=1.5)
+    ids, w, _ = orc.topk_from_logits(orc.round_bf16(lg), k)
+    g = torch.Generator(device=dev).manual_seed(9)
+    w13 = (torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    out = pkg.experts_bf16(to_bf16(x, dev), to_dev(ids, dev), to_bf16(w, dev), w13, w2)
+    sub, n_tiles = tile_stratified_tokens(ids, E, 128, rng)
+    assert n_tiles > 200
+    ref = orc.experts_bf16(x[sub], ids[sub], w[sub], np_f32(w13), np_f32(w2), acc=np.float32)
+    got = np_f32(out)[sub]
+    max_abs, mean_rel = errors(got, ref)
+    assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
     assert (bf16_ulp_diff(got, ref) == 0).mean() >= 0.95
 
 
