@@ -297,6 +297,11 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     const uint4 v_ = *(const uint4*)(sB_ + (PF_BROW(ni_) - lr) * 128 + ((h_) ? frag_off1 : frag_off0)); \
     B_[ni_][4 * (h_)] = v_.x; B_[ni_][4 * (h_) + 1] = v_.y; B_[ni_][4 * (h_) + 2] = v_.z; B_[ni_][4 * (h_) + 3] = v_.w; \
   } while (0)
+// An empty volatile asm that takes and returns v_: the value is computed before this point
+// and the volatile asm statements keep their order, which holds each MFMA and each scale FMA in
+// its slot (sched_barrier alone binds only the machine scheduler: without the pins the FMAs
+// were sunk below all 16 MFMAs, every MFMA result stayed live and the step lost its overlap).
+#define PF_PIN(v_) asm volatile("" : "+v"(v_))
 #define PF_STEP_BODY(AC, AN, B, SC, SN, WC, WN, st_, j1_, kb1_, ab_, bb_, sab_, sbw_)             \
   do {                                                                                            \
     const uint8_t* sA_ = s_ab[st_];                                                               \
@@ -312,6 +317,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       if (it < 16) {                                                                              \
         const int ni = it >> 2, mi = it & 3;                                                      \
         t_[it & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(B[ni], AC[mi], zero4, 0, 0, 0, 0, 0, 0); \
+        PF_PIN(t_[it & 3]);                                                                       \
       }                                                                                           \
       switch (it) {                                                                               \
         case 0: PF_RD_A(AN, 0, 0); break;                                                         \
@@ -347,6 +353,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
         const int j = it - 3, ni = j >> 2, mi = j & 3;                                            \
         const float sc_ = (MODE == PF_GATE_UP && ni >= 2) ? scb_[mi] : sca_[mi];                  \
         _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[mi][ni][q] = fmaf(t_[j & 3][q], sc_, acc[mi][ni][q]); \
+        PF_PIN(acc[mi][ni]);                                                                      \
       }                                                                                           \
       __builtin_amdgcn_sched_barrier(0);                                                          \
     }                                                                                             \
@@ -567,6 +574,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
   }
 #undef PF_STEP
 #undef PF_STEP_BODY
+#undef PF_PIN
 #undef PF_STEP_BODY_BF
 #undef PF_RD_A
 #undef PF_RD_B
