@@ -40,6 +40,7 @@ sys.path.insert(0, REPO)
 METRIC = "MoE layer µs + % roofline (HBM GB/s / FP8 MFMA), Qwen3-30B-A3B shape, bs 1–4096"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 LLC_BYTES = 256 * 2 ** 20
 K_TOP = 8
 N_SLOTS = 8  # kernel timing slots of the library (include/moe_mi355x.h)
@@ -83,6 +84,13 @@ class Shape:
     def expected_active(self, T):
         return self.E * (1.0 - (1.0 - K_TOP / self.E) ** T)
 
+    def bf16_gate_up_bytes(self, n_active, T):
+        """bf16 experts: the active experts' W13, x read, bf16 h written."""
+        return n_active * 2 * (2 * self.I * self.H) + 2 * T * self.H + 2 * T * K_TOP * self.I
+
+    def bf16_layer_bytes(self, n_active, T):
+        return n_active * 2 * 3 * self.I * self.H + 2 * self.E * self.H + 4 * T * self.H
+
     def prefill_path(self, T):
         """True where the library picks the 128-row MFMA-tiled (compute-bound) GEMMs."""
         return T * K_TOP > 16 * self.E and self.H % 256 == 0
@@ -125,6 +133,24 @@ class Layer:
         return max(2, min(len(self.copies), math.ceil(2 * LLC_BYTES / max(1.0, per_step))))
 
 
+class Bf16Layer:
+    """Router + bf16 experts of one shape (the reference's default checkpoint dtype, run on the
+    library's bf16 path), with `n_copies` distinct copies of the experts."""
+
+    def __init__(self, torch, dev, shape, n_copies, wr):
+        self.shape = shape
+        self.wr = wr
+        g = torch.Generator(device=dev).manual_seed(7)
+        self.copies = []
+        for _ in range(n_copies):
+            w13 = (torch.randn((shape.E, 2 * shape.I, shape.H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            w2 = (torch.randn((shape.E, shape.H, shape.I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            self.copies.append((w13, w2))
+
+    def n_rot(self, T):
+        return len(self.copies)
+
+
 def make_inputs(torch, dev, shape, T, n, zipf_beta=None):
     g = torch.Generator(device=dev).manual_seed(1000 + T)
     xs = [torch.randn((T, shape.H), generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
@@ -164,13 +190,14 @@ def calibrate_zipf(pkg, torch, dev, layer, T=4096):
 
 def run_config(pkg, torch, layer, T, steps, warmup, router, xs):
     """Times `steps` block forwards, then runs them again under the library's per-kernel
-    HIP events.  Returns (ms per step, per-slot average ms, mean active experts, copies)."""
+    HIP events.  Returns (ms per step, per-slot average ms, mean active experts, copies).
+    A Bf16Layer runs the bf16-expert block, a Layer the FP8 one."""
     lib = pkg._lib.load()
     n_rot = layer.n_rot(T)
+    block = pkg.moe_block_bf16 if isinstance(layer, Bf16Layer) else pkg.moe_block_fp8
 
     def step(i, routing=False):
-        q13, s13, q2, s2 = layer.copies[i % n_rot]
-        return pkg.moe_block_fp8(xs[i % len(xs)], router, K_TOP, q13, s13, q2, s2, return_routing=routing)
+        return block(xs[i % len(xs)], router, K_TOP, *layer.copies[i % n_rot], return_routing=routing)
 
     for i in range(warmup):
         step(i)
@@ -249,6 +276,42 @@ def roofline_for(shape, T, slots, n_active):
             "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
 
 
+def bf16_sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
+    """The bf16-expert block (the reference's default bf16 checkpoint, no FP8 requantisation):
+    decode batches are HBM-bound, the 128-row prefill tiles bf16-MFMA-bound."""
+    shape = layer.shape
+    beta = share = None
+    router = layer.wr
+    if zipf is not None:
+        beta, share = zipf
+        router = zipf_router(torch, layer.wr, beta)
+    xs = make_inputs(torch, dev, shape, T, 4, zipf_beta=beta)
+    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 3, router, xs)
+    dur_ms = slots["gemm_gate_up"]
+    entry = {"shape": shape.name, "experts_dtype": "bf16", "tokens": T, "us_per_layer": round(ms * 1e3, 2),
+             "tokens_per_s": round(T / (ms * 1e-3), 1), "mean_active_experts": round(act, 2),
+             "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()}}
+    if shape.prefill_path(T):
+        flops = shape.gate_up_flops(T)
+        achieved = flops / dur_ms / 1e9
+        entry["roofline"] = {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
+                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                             "traffic": None, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+        entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
+        entry["layer_bf16_peak_frac"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)
+    else:
+        byts = shape.bf16_gate_up_bytes(act, T)
+        achieved = byts / (dur_ms * 1e-3) / 1e9
+        entry["roofline"] = {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                             "traffic": None, "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
+        entry["layer_hbm_frac"] = round(shape.bf16_layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if zipf is not None:
+        entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
+    print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
+    return entry
+
+
 def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
     shape = layer.shape
     beta = share = None
@@ -258,7 +321,7 @@ def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
         router = zipf_router(torch, layer.wr, beta)
     xs = make_inputs(torch, dev, shape, T, 4, zipf_beta=beta)
     ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 5, router, xs)
-    entry = {"shape": shape.name, "tokens": T, "us_per_layer": round(ms * 1e3, 2),
+    entry = {"shape": shape.name, "experts_dtype": "fp8", "tokens": T, "us_per_layer": round(ms * 1e3, 2),
              "tokens_per_s": round(T / (ms * 1e-3), 1),
              "us_per_layer_graph": round(graph_step_ms(pkg, torch, layer, T, steps, router, xs) * 1e3, 2),
              "mean_active_experts": round(act, 2), "roofline": roofline_for(shape, T, slots, act),
@@ -419,6 +482,9 @@ def main():
     ap.add_argument("--decode-step-only", action="store_true", help="run only the 48-layer decode step")
     ap.add_argument("--shape", choices=["30b", "235b"], default="30b",
                     help="layer of the headline line: Qwen3-30B-A3B (default) or Qwen3-235B-A22B")
+    ap.add_argument("--experts-dtype", choices=["fp8", "bf16"], default="fp8",
+                    help="bf16: time only the bf16-expert block of the 30B layer at --tokens (one JSON "
+                         "entry, for profiling); the headline line is always the FP8 block")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (expert-parallel sharding "
@@ -442,6 +508,14 @@ def main():
         del src, dst
     if args.decode_step_only:
         print(json.dumps({"decode_step": decode_step_entry(pkg, torch, dev)}), flush=True)
+        return
+    if args.experts_dtype == "bf16":
+        g = torch.Generator(device=dev).manual_seed(0)
+        wr = (torch.randn((S30B.E, S30B.H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        b16 = Bf16Layer(torch, dev, S30B, 2, wr)
+        zipf = calibrate_zipf(pkg, torch, dev, b16, T=args.tokens) if args.zipf else None
+        print(json.dumps({"bf16_block": bf16_sweep_entry(pkg, torch, dev, b16, args.tokens, args.steps, zipf=zipf)}),
+              flush=True)
         return
     layer = Layer(pkg, torch, dev, S30B, n_copies=16) if args.shape == "30b" else Layer(pkg, torch, dev, S235B, n_copies=2)
     shape = layer.shape
@@ -490,6 +564,13 @@ def main():
         for Ts in (64, 2048):
             sweep.append(sweep_entry(pkg, torch, dev, big, Ts, 20 if Ts < 2048 else 10))
         del big
+        torch.cuda.empty_cache()
+        b16 = Bf16Layer(torch, dev, S30B, 2, layer.wr)
+        for Ts in (1, 64, 4096):
+            sweep.append(bf16_sweep_entry(pkg, torch, dev, b16, Ts, 20 if Ts < 4096 else 10,
+                                          zipf=zipf if Ts == 4096 else None))
+        del b16
+        torch.cuda.empty_cache()
         line["sweep"] = sweep
     if not args.no_decode_step and not args.no_sweep:
         del layer.copies[1:]

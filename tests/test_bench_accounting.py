@@ -62,3 +62,12 @@ def test_weight_rotation_defeats_the_last_level_cache():
         n = layer.n_rot(T)
         per_step = layer.shape.layer_bytes(layer.shape.expected_active(T), T)
         assert 2 <= n <= 16 and (n - 1) * per_step >= bench.LLC_BYTES, (T, n)
+
+
+def test_bf16_bytes():
+    """bf16 experts: 2 bytes per weight, no scales: gate_up streams 2 * 2I * H per active expert
+    (6,291,456 B at the 30B shape) plus x in and bf16 h out; the layer adds W2 and the router."""
+    s = bench.S30B
+    assert s.bf16_gate_up_bytes(1, 1) == 2 * 2 * 768 * 2048 + 2 * 2048 + 2 * 8 * 768
+    assert s.bf16_gate_up_bytes(126, 64) == 126 * 6_291_456 + 2 * 64 * 2048 + 2 * 512 * 768
+    assert s.bf16_layer_bytes(126, 64) == 126 * 9_437_184 + 2 * 128 * 2048 + 4 * 64 * 2048
