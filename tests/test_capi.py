@@ -80,3 +80,41 @@ def test_argument_validation_before_launch(lib):
     # null tensors with T > 0 are rejected
     assert lib.moe_mi355x_experts_fp8(null, null, 4, null, 1, 2048, 768, 128, 8, null, null, null, null, null,
                                       null, 0, null) == -1
+
+
+def test_bf16_noalloc_and_numerics_queries(lib):
+    """Host-side queries and argument checks of the bf16, no-allocation and sublayer entry points
+    (no device work: every case returns before a launch)."""
+    null = None
+    fake = 0x10000  # a 16-byte-aligned address that is never dereferenced on these paths
+    assert lib.moe_mi355x_experts_bf16_workspace_bytes(64, 2048, 768, 128, 8) > 64 * 8 * 2048 * 2
+    assert lib.moe_mi355x_experts_bf16_workspace_bytes(64, 2000, 768, 128, 8) == 0
+    assert lib.moe_mi355x_block_bf16_workspace_bytes(64, 2048, 768, 128, 8) > \
+        lib.moe_mi355x_experts_bf16_workspace_bytes(64, 2048, 768, 128, 8)
+    assert lib.moe_mi355x_moe_sublayer_workspace_bytes(64, 2048, 768, 128, 8) > \
+        lib.moe_mi355x_block_workspace_bytes(64, 2048, 768, 128, 8)
+    # bf16 experts: unsupported shape, T == 0 no-op, null tensors
+    assert lib.moe_mi355x_experts_bf16(null, null, 4, null, 4, 2000, 768, 128, 8, null, null, null, null, 0,
+                                       null) == -1
+    assert lib.moe_mi355x_experts_bf16(null, null, 4, null, 0, 2048, 768, 128, 8, null, null, null, null, 0,
+                                       null) == 0
+    assert lib.moe_mi355x_experts_bf16(null, null, 4, null, 1, 2048, 768, 128, 8, null, null, null, null, 0,
+                                       null) == -1
+    assert lib.moe_mi355x_block_bf16(null, null, 1, 2048, 768, 128, 8, 1, null, null, null, null, null, 4, null,
+                                     null, 0, null) == -1
+    # no-allocation block: 64 MiB of scratch; a call needing more returns MOE_ERR_SCRATCH (-4)
+    assert lib.moe_mi355x_block_fp8_noalloc_scratch_bytes() == 64 << 20
+    assert lib.moe_mi355x_block_workspace_bytes(4096, 4096, 1536, 128, 8) > 64 << 20
+    assert lib.moe_mi355x_block_fp8_noalloc(fake, fake, 4096, 4096, 1536, 128, 8, 1, fake, fake, fake, fake, fake,
+                                            null, null, 4, null, null) == -4
+    assert b"scratch" in lib.moe_mi355x_error_string(-4)
+    assert lib.moe_mi355x_block_fp8_noalloc(null, null, 1, 2048, 768, 128, 8, 1, null, null, null, null, null,
+                                            null, null, 4, null, null) == -1
+    # tile height (low 16 bits of the numerics key): 16-row up to 8 pairs per expert, 32-row up to
+    # 16, then the 128-row LDS-tiled kernels (FP8 and bf16 alike at the 30B shape)
+    for fp8 in (1, 0):
+        bm = {t: int(lib.moe_mi355x_block_numerics_key(t, 2048, 768, 128, 8, fp8)) & 0xFFFF
+              for t in (1, 128, 129, 256, 257, 4096)}
+        assert bm == {1: 16, 128: 16, 129: 32, 256: 32, 257: 128, 4096: 128}, (fp8, bm)
+    # bf16 above 16 pairs per expert with H % 256 != 0: 64-row tiles
+    assert int(lib.moe_mi355x_block_numerics_key(100, 384, 256, 8, 2, 0)) & 0xFFFF == 64
