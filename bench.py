@@ -63,12 +63,12 @@ class Shape:
 
     def gate_up_bytes(self, n_active, T):
         """Algorithmic HBM bytes of one gate_up launch: the active experts' W13 + scales,
-        the fp8 activations and their scales read, the intermediate written (on 16-row tiles,
-        S <= 8 E, the launch quantises it itself: e4m3 codes + scales, and its bf16 h
+        the fp8 activations and their scales read, the intermediate written (up to 2 pairs per
+        expert, S <= 2 E, the launch quantises it itself: e4m3 codes + scales, and its bf16 h
         round trip between the launch's workgroups is counted too; otherwise bf16 h)."""
         S = T * K_TOP
         out = 2 * S * self.I
-        if S <= 8 * self.E:
+        if S <= 2 * self.E:
             out += 2 * S * self.I + S * self.I + 4 * S * (self.I // 128)
         return n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128) + out
 
@@ -102,11 +102,11 @@ S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 # HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy):
 #   decode 64:            rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} ... -- python3 bench.py --no-sweep --no-cpu
-#                         --steps 10 --warmup 2 --copy-probe           -> 195,732 / 1,381 KiB
+#                         --steps 10 --warmup 2 --copy-probe           -> 195,241 / 768 KiB
 #   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
 #                         --copy-probe                                 -> 291,674 / 25,447 KiB
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): 195732 * 1024 * 2 + 1381 * 1024,
+    ("qwen3-30b-a3b", 64): 195241 * 1024 * 2 + 768 * 1024,
     ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
 }
 

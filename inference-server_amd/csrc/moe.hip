@@ -192,12 +192,15 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
   }
   // the hand-offs pay on 16-row tiles (batches up to 8 pairs per expert): fewer launches outweigh
   // each workgroup's wait for its stores; on 32-row tiles the separate launches are faster
-  // (Qwen3-30B-A3B layer at 256 tokens: 163 against 172 us)
+  // (Qwen3-30B-A3B layer at 256 tokens: 163 against 172 us).  The h quantisation's hand-off pays
+  // only up to 2 pairs per expert: above, the separate quant_h launch is faster (64 tokens: 130.5
+  // against 133 us, 128 tokens: 141 against 144 us; level at 8-32 tokens)
   const bool decode = w.block_m == 16;
+  const bool quant_handoff = decode && S <= 2 * E;
   const bool fused_combine = decode && ids_valid;
   rc = moe_launch_grouped_gemms(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2, w.perm, w.tiles,
                                 w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.hq, w.sh, w.pairs, S, H,
-                                I, k, w.block_m, s, decode ? w.cnt : nullptr,
+                                I, k, w.block_m, s, quant_handoff ? w.cnt : nullptr,
                                 fused_combine ? w.cnt + (long)w.max_tiles * (I / MOE_GROUP) : nullptr, (uint16_t*)out,
                                 (const uint16_t*)residual);
   if (rc) return rc;
