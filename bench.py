@@ -92,8 +92,9 @@ class Shape:
         return n_active * 2 * 3 * self.I * self.H + 2 * self.E * self.H + 4 * T * self.H
 
     def prefill_path(self, T):
-        """True where the library picks the 128-row MFMA-tiled (compute-bound) GEMMs."""
-        return T * K_TOP > 16 * self.E and self.H % 256 == 0
+        """True where the library picks the 128-row MFMA-tiled (compute-bound) GEMMs: beyond 8
+        pairs per expert, for a hidden size in 256-column tiles and both GEMMs >= 4 K blocks."""
+        return T * K_TOP > 8 * self.E and self.H % 256 == 0 and self.H >= 512 and self.I >= 512
 
 
 S30B = Shape("qwen3-30b-a3b", 2048, 768)

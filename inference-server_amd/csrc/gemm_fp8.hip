@@ -399,16 +399,17 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
                                      const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w, uint8_t* hq,
                                      float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s);
 
-// Tile height (rows per M tile) for S pairs over E experts: 16- or 32-row tiles stream
-// weights (decode); 128-row tiles go to the LDS-tiled MFMA kernel (prefill, needs H % 256 == 0).
+// Tile height (rows per M tile) for S pairs over E experts: 16-row tiles stream weights
+// (decode); beyond 8 pairs per expert 128-row tiles go to the LDS-tiled MFMA kernel (needs
+// 256-column tiles of H and at least 4 K blocks in each GEMM for its cross-item DMA pipeline):
+// from 9 to 16 pairs per expert it also beats 32-row streaming tiles (30B layer: 192 tokens
+// 158 -> 150 us, 256 tokens 161 -> 151 us, level at 129).  Shapes it cannot take stream 32-row
+// tiles up to 16 pairs per expert (one tile per expert for the usual loads instead of two 16-row
+// ones) and 64-row tiles above.
 int moe_gemm_block_m(int S, int E, int H, int I) {
   if (S <= 8 * E) return 16;
-  // beyond 8 pairs per expert on average, 16-row tiles would split many experts in two and
-  // stream their weights twice: 32-row tiles keep one tile per expert for the usual loads
-  if (S <= 16 * E) return 32;
-  // the 128-row prefill path: 256-column tiles of H, and at least 4 K blocks in each GEMM
-  // for its cross-item DMA pipeline
-  return H % 256 == 0 && H >= 512 && I >= 512 ? 128 : 64;
+  if (H % 256 == 0 && H >= 512 && I >= 512) return 128;
+  return S <= 16 * E ? 32 : 64;
 }
 
 // Column blocks of the decode down GEMM for S pairs at tile height block_m: the width of the

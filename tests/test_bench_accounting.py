@@ -45,11 +45,11 @@ def test_expected_active_experts(T, expected):
 
 def test_prefill_path_matches_library_choice():
     """bench labels a configuration MFMA-bound exactly where the library runs the 128-row
-    prefill GEMM (16-row tiles up to 8 pairs per expert, 32-row up to 16, then 128-row)."""
+    prefill GEMM (16-row tiles up to 8 pairs per expert, then 128-row at these shapes)."""
     for shape in (bench.S30B, bench.S235B):
         for T in (1, 64, 128, 256, 257, 1024, 4096):
             S = T * bench.K_TOP
-            bm = 16 if S <= 8 * shape.E else 32 if S <= 16 * shape.E else 128
+            bm = 16 if S <= 8 * shape.E else 128
             assert shape.prefill_path(T) == (bm == 128), (shape.name, T)
 
 

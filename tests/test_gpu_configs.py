@@ -5,7 +5,8 @@ reference's golden vectors.
   top-k ids that transformers' ``Qwen3MoeSparseMoeBlock`` wrote on CPU
   (tests/golden/make_golden.py), and the FP8 block on the same inputs against the oracle.
 * C2: decode batches including 128 and 129 tokens, the 8 E pair count where the expert GEMMs
-  switch from 16- to 32-row tiles (tests/test_gpu_parity.py covers 1, 8, 32, 64, 256).
+  switch from 16-row streaming tiles to the 128-row LDS-tiled kernel, and 256 tokens
+  (tests/test_gpu_parity.py covers 1, 8, 32, 64, 256).
 * C3: the 4096-token Zipf-skewed prefill chunk, checked on a tile-stratified token sample: the
   first, the last and a random row of every M tile of the expert GEMMs (ragged remainders of the
   cold experts included) belong to a checked token.
@@ -145,10 +146,11 @@ def w30b(dev):
     return wd, host_weights(wd)
 
 
-@pytest.mark.parametrize("T", [127, 128, 129])
+@pytest.mark.parametrize("T", [127, 128, 129, 256])
 def test_c2_decode_tile_switch(pkg, dev, w30b, T):
-    """Around S = 8 E = 1024 pairs: 16-row tiles up to 128 tokens, 32-row tiles from 129."""
-    assert block_m_of(pkg, T, 2048, 768, 128, 8) == (16 if T <= 128 else 32)
+    """Around S = 8 E = 1024 pairs: 16-row tiles up to 128 tokens, the 128-row LDS-tiled kernel
+    from 129 (every token checked)."""
+    assert block_m_of(pkg, T, 2048, 768, 128, 8) == (16 if T <= 128 else 128)
     rng = np.random.default_rng(200 + T)
     x = orc.gen_normal_bf16(rng, (T, 2048))
     ids, w = orc.uniform_routing(rng, T, 128, 8)

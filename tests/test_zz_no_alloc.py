@@ -53,8 +53,8 @@ def _call_pair(lib, x, wr, k, weights, dev):
 @pytest.mark.gpu
 @pytest.mark.parametrize("H,I,T1,T2", [(2048, 768, 300, 40), (4096, 1536, 64, 1)])
 def test_noalloc_block_equals_workspace_block(pkg, dev, H, I, T1, T2):
-    """Qwen3-30B-A3B shape (300 tokens: 32-row tiles, then 40: 16-row tiles) and Qwen3-235B-A22B
-    shape (decode 64, then 1 token)."""
+    """Qwen3-30B-A3B shape (300 tokens: the 128-row LDS-tiled GEMMs, then 40: 16-row tiles) and
+    Qwen3-235B-A22B shape (decode 64, then 1 token)."""
     lib = pkg._lib.load()
     E, k = 128, 8
     weights = gpu_weights(E, H, I, dev, seed=31)
