@@ -111,13 +111,13 @@ def test_bf16_noalloc_and_numerics_queries(lib):
     assert lib.moe_mi355x_block_fp8_noalloc(null, null, 1, 2048, 768, 128, 8, 1, null, null, null, null, null,
                                             null, null, 4, null, null) == -1
     # tile height (low 16 bits of the numerics key): 16-row up to 8 pairs per expert, then the
-    # 128-row LDS-tiled kernel (FP8); bf16 streams 32-row tiles up to 16 pairs per expert
-    bm = {t: int(lib.moe_mi355x_block_numerics_key(t, 2048, 768, 128, 8, 1)) & 0xFFFF
-          for t in (1, 128, 129, 256, 257, 4096)}
-    assert bm == {1: 16, 128: 16, 129: 128, 256: 128, 257: 128, 4096: 128}, bm
-    bm = {t: int(lib.moe_mi355x_block_numerics_key(t, 2048, 768, 128, 8, 0)) & 0xFFFF
-          for t in (1, 128, 129, 256, 257, 4096)}
-    assert bm == {1: 16, 128: 16, 129: 32, 256: 32, 257: 128, 4096: 128}, bm
+    # 128-row LDS-tiled kernels (FP8 and bf16 alike at the 30B shape)
+    for fp8 in (1, 0):
+        bm = {t: int(lib.moe_mi355x_block_numerics_key(t, 2048, 768, 128, 8, fp8)) & 0xFFFF
+              for t in (1, 128, 129, 256, 257, 4096)}
+        assert bm == {1: 16, 128: 16, 129: 128, 256: 128, 257: 128, 4096: 128}, (fp8, bm)
+    # bf16 shapes the 128-row kernel cannot take: 32-row tiles up to 16 pairs per expert
+    assert int(lib.moe_mi355x_block_numerics_key(37, 384, 256, 20, 5, 0)) & 0xFFFF == 32
     # FP8 shapes the 128-row kernel cannot take: 32-row tiles up to 16 pairs per expert, 64 above
     assert int(lib.moe_mi355x_block_numerics_key(30, 384, 256, 6, 3, 1)) & 0xFFFF == 32
     assert int(lib.moe_mi355x_block_numerics_key(100, 384, 256, 6, 3, 1)) & 0xFFFF == 64
