@@ -415,7 +415,7 @@ int moe_gemm_block_m(int S, int E, int H, int I) {
 // Column blocks of the decode down GEMM for S pairs at tile height block_m: the width of the
 // per-token hand-off counters (tok_cnt [T, blocks]).
 int moe_down_col_blocks(int S, int H, int block_m) {
-  if (block_m == 16) return S > 64 ? H / 64 : H / 32;  // CG 2 x 16 DN columns
+  if (block_m == 16) return S > 16 ? H / 64 : H / 32;  // CG 2 x 16 DN columns
   if (block_m == 32) return H / 128;                   // CG 4 x 32 columns
   return H / 64;                                       // CG 4 x 16 columns
 }
@@ -451,8 +451,9 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   }
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, nullptr, nullptr, nullptr,
               tok_cnt, comb, residual};
-  if (block_m == 16)  // beyond a few tokens, two column slices per wave stream more bytes per setup
-    rc = S > 64 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  if (block_m == 16)  // beyond 2 tokens two column slices per wave stream more bytes per setup
+    // (T=8: down 25.7 -> 24.9 us; level at 1, 32 and 64 tokens)
+    rc = S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
   else if (block_m == 32)
     rc = launch_gemm<MODE_DOWN, 2, 1, 2, true>(g2, max_tiles, s);
   else
