@@ -92,7 +92,7 @@ extern "C" int moe_mi355x_align_max_tiles(int S, int E, int block_m) {
 }
 
 extern "C" size_t moe_mi355x_align_workspace_bytes(int S, int E) {
-  if (S <= kSingleMaxS) return 0;
+  if (S <= kAlignOneWgMaxS) return 0;
   const size_t nb = (S + kChunk - 1) / kChunk;
   return moe_align_up(nb * (E + 1) * sizeof(int32_t), 256);
 }
@@ -105,7 +105,7 @@ int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int bl
 int moe_launch_align(const void* ids, int id_bytes, int S, int E, int block_m, int32_t* perm,
                      int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles, void* workspace,
                      size_t workspace_bytes, hipStream_t s, int32_t* zero, int nzero) {
-  if (S <= kSingleMaxS) {
+  if (S <= kAlignOneWgMaxS) {
     MOE_LAUNCH(MOE_PROF_ALIGN, s, align_single_kernel, dim3(1), dim3(kChunk), 0, s, ids, id_bytes, S, E, block_m, perm,
                        counts, offsets, tiles, n_tiles, zero, nzero);
     MOE_CHECK_LAUNCH();

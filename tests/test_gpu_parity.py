@@ -113,6 +113,7 @@ def test_route(pkg, dev, T, H, E, k):
 
 
 @pytest.mark.parametrize("T,k,E,block_m", [(1, 8, 128, 16), (16, 8, 128, 16), (64, 8, 128, 16),
+                                           (256, 8, 128, 128), (257, 8, 128, 128),  # one WG / chunked
                                            (512, 8, 128, 16), (513, 8, 128, 64), (4096, 8, 128, 64),
                                            (3000, 4, 60, 32), (4096, 8, 128, 256), (0, 8, 128, 16)])
 @pytest.mark.parametrize("index_dtype", [np.int32, np.int64])
