@@ -193,6 +193,67 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// The token combine of a down-GEMM workgroup on the hand-off path, run by its last result wave
+// once the workgroup's pair rows (columns [bx CB, (bx + 1) CB) of its tile's rows) are stored
+// device-scope: one tile row (pair) per lane counts in for its token's column block in tok_cnt
+// [T, nbx] (zero on entry); the lanes whose count completes the token's k slots list their
+// tokens (s_tok, one int per lane), and the wave sums each listed token's k pair rows over the
+// block's columns: fp32 in slot order, + residual (bf16, when non-null) after one bf16 rounding,
+// one bf16 rounding into comb [T, N] (combine_kernel's arithmetic).
+template <int CB>
+__device__ __forceinline__ void handoff_combine(const int32_t* perm, int topk, int row0, int rows, int32_t* tok_cnt,
+                                                int nbx, int bx, const uint16_t* pairs, int N,
+                                                const uint16_t* residual, uint16_t* comb, int* s_tok) {
+  const int lane = threadIdx.x & 63;
+  bool done = false;
+  int t = 0;
+  if (lane < rows) {
+    t = perm[row0 + lane] / topk;
+    done = xwg_count_in(tok_cnt + (long)t * nbx + bx) == topk - 1;
+  }
+  const uint64_t mask = __ballot(done);
+  if (done) s_tok[__popcll(mask & lanemask_lt())] = t;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const int ntok = __popcll(mask);
+  constexpr int PER_TOK = CB / 8;
+  for (int u = lane; u < ntok * PER_TOK; u += MOE_WAVE) {
+    const int tt = s_tok[u / PER_TOK];
+    const int c0 = bx * CB + (u % PER_TOK) * 8;
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < topk; j0 += 8) {
+      uint4 rv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rv[j] = xwg_load128(pairs + (long)(tt * topk + min(j0 + j, topk - 1)) * N + c0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j0 + j >= topk) break;
+        const uint32_t w4[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sum[2 * i] += __uint_as_float(w4[i] << 16);
+          sum[2 * i + 1] += __uint_as_float(w4[i] & 0xffff0000u);
+        }
+      }
+    }
+    if (residual != nullptr) {
+      const uint4 r4 = *(const uint4*)(residual + (long)tt * N + c0);
+      const uint32_t ru[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sum[2 * i] = __uint_as_float(ru[i] << 16) + round_bf16(sum[2 * i]);
+        sum[2 * i + 1] = __uint_as_float(ru[i] & 0xffff0000u) + round_bf16(sum[2 * i + 1]);
+      }
+    }
+    uint4 o4;
+    o4.x = (uint32_t)f32_to_bf16(sum[0]) | ((uint32_t)f32_to_bf16(sum[1]) << 16);
+    o4.y = (uint32_t)f32_to_bf16(sum[2]) | ((uint32_t)f32_to_bf16(sum[3]) << 16);
+    o4.z = (uint32_t)f32_to_bf16(sum[4]) | ((uint32_t)f32_to_bf16(sum[5]) << 16);
+    o4.w = (uint32_t)f32_to_bf16(sum[6]) | ((uint32_t)f32_to_bf16(sum[7]) << 16);
+    *(uint4*)(comb + (long)tt * N + c0) = o4;
+  }
+}
+
 // Read an expert id stored as int32 or int64.
 __device__ __forceinline__ int load_id(const void* ids, int id_bytes, int i) {
   return id_bytes == 8 ? (int)((const int64_t*)ids)[i] : ((const int32_t*)ids)[i];

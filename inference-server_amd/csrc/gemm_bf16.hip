@@ -36,6 +36,11 @@ struct Bf16GemmArgs {
   int K;                   // reduction length (multiple of 128)
   int N;                   // output columns (gate_up: I, down: H)
   int topk;
+  // down, hand-off (null: off): the pair rows are stored device-scope and each token's k rows are
+  // summed in slot order into comb by the workgroup that completes the token's column block
+  // (tok_cnt [T, column blocks], zero on entry; every id must be valid)
+  int32_t* tok_cnt;
+  uint16_t* comb;
 };
 
 typedef uint4 Frag[4];  // the four 16-byte pieces of one lane for a 128-deep K block
@@ -61,6 +66,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
 
   __shared__ int s_arow[BM];
   __shared__ float s_red[KS > 1 ? (KS - 1) * CG * WM * NOP * 4 * 64 : 1];
+  __shared__ int s_done;     // down hand-off: result waves past their stores
+  __shared__ int s_tok[BM];  // down hand-off: tokens this workgroup combines
+  if (threadIdx.x == 0) s_done = 0;  // visible after the row-setup barrier
 
   // weight rows of this lane (gate_up: the up rows follow the I gate rows)
   const uint16_t* bptr[NOP];
@@ -156,6 +164,49 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
   }
 
   const int col = n0 + lr;
+  if constexpr (MODE == MODE_DOWN) {
+    if (p.tok_cnt != nullptr) {  // workgroup-uniform
+      static_assert(BM <= MOE_WAVE, "one tile row per lane");
+      // device-coherent stores: lanes lr and lr ^ 1 hold adjacent columns of the same rows, so the
+      // even lane stores rows q = 0, 1 and the odd lane rows 2, 3 as 32-bit stores of both columns
+      const bool odd = lr & 1;
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi) {
+        uint32_t v[NOP][4];
+        int dst[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int pair = p.perm[row0 + min(mi * 16 + 4 * lg + q, rows - 1)];
+          const float wt = bf16_to_f32(p.topk_w[pair]);
+#pragma unroll
+          for (int o = 0; o < NOP; ++o) v[o][q] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
+          dst[q] = pair;
+        }
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) {
+          uint32_t pv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pv[q] = (uint32_t)__shfl_xor((int)v[o][q], 1);
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int q = odd ? 2 + h2 : h2;
+            if (mi * 16 + 4 * lg + q >= rows) continue;
+            const uint32_t both = odd ? (pv[q] | (v[o][q] << 16)) : (v[o][q] | (pv[q] << 16));
+            xwg_store32(p.out + (long)dst[q] * p.N + (col & ~1) + 16 * o, both);
+          }
+        }
+      }
+      // each result wave waits for its stores; the last of the CG to get there combines
+      xwg_wait_stores();
+      int order = 0;
+      if (lane == 0) order = atomicAdd(&s_done, 1);
+      order = __builtin_amdgcn_readfirstlane(order);
+      if (order != CG - 1) return;
+      handoff_combine<CG * WCOLS>(p.perm, p.topk, row0, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N,
+                                  nullptr, p.comb, s_tok);
+      return;
+    }
+  }
 #pragma unroll
   for (int mi = 0; mi < WM; ++mi) {
 #pragma unroll
@@ -210,10 +261,10 @@ int moe_bf16_block_m(int S, int E, int H, int I) {
 int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2, const int32_t* perm,
                                   const int32_t* tiles, const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w,
                                   uint16_t* h, uint16_t* pairs, int S, int H, int I, int k, int block_m,
-                                  hipStream_t s) {
+                                  hipStream_t s, int32_t* tok_cnt, uint16_t* comb) {
   if (block_m == 128)
     return moe_launch_grouped_gemms_prefill_bf16(x, w13, w2, perm, tiles, n_tiles, max_tiles, h, pairs, H, I, k, s);
-  Bf16GemmArgs g1{x, w13, perm, tiles, n_tiles, nullptr, h, H, I, k};
+  Bf16GemmArgs g1{x, w13, perm, tiles, n_tiles, nullptr, h, H, I, k, nullptr, nullptr};
   int rc;
   if (block_m == 16)
     rc = launch_bf16_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
@@ -222,7 +273,8 @@ int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const 
   else
     rc = launch_bf16_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
-  Bf16GemmArgs g2{h, w2, perm, tiles, n_tiles, topk_w, pairs, I, H, k};
+  // the token-combine hand-off on 16-row tiles (tok_cnt [T, H / 64]: CG 2 x 32 columns)
+  Bf16GemmArgs g2{h, w2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, block_m == 16 ? tok_cnt : nullptr, comb};
   if (block_m == 16)
     rc = launch_bf16_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s);
   else if (block_m == 32)

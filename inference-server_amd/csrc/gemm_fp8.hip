@@ -322,59 +322,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
       }
     }
   } else {
-    // one tile row (pair) per lane counts in for its token's column block; the lanes whose count
-    // completes the token's k slots list their tokens, and this wave sums each listed token's k
-    // rows over the workgroup's columns: fp32 in slot order, the residual add, one bf16 rounding
     static_assert(BM <= MOE_WAVE, "one tile row per lane");
-    bool done = false;
-    int t = 0;
-    if (lane < rows) {
-      t = p.perm[row0 + lane] / p.topk;
-      done = xwg_count_in(p.tok_cnt + (long)t * gridDim.x + blockIdx.x) == p.topk - 1;
-    }
-    const uint64_t mask = __ballot(done);
-    if (done) s_tok[__popcll(mask & lanemask_lt())] = t;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    const int ntok = __popcll(mask);
-    constexpr int CB = CG * WCOLS;  // this workgroup's output columns
-    constexpr int PER_TOK = CB / 8;
-    for (int u = lane; u < ntok * PER_TOK; u += MOE_WAVE) {
-      const int tt = s_tok[u / PER_TOK];
-      const int c0 = blockIdx.x * CB + (u % PER_TOK) * 8;
-      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int j0 = 0; j0 < p.topk; j0 += 8) {
-        uint4 rv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          rv[j] = xwg_load128(p.out + (long)(tt * p.topk + min(j0 + j, p.topk - 1)) * p.N + c0);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j0 + j >= p.topk) break;
-          const uint32_t w4[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sum[2 * i] += __uint_as_float(w4[i] << 16);
-            sum[2 * i + 1] += __uint_as_float(w4[i] & 0xffff0000u);
-          }
-        }
-      }
-      if (p.residual != nullptr) {
-        const uint4 r4 = *(const uint4*)(p.residual + (long)tt * p.N + c0);
-        const uint32_t ru[4] = {r4.x, r4.y, r4.z, r4.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sum[2 * i] = __uint_as_float(ru[i] << 16) + round_bf16(sum[2 * i]);
-          sum[2 * i + 1] = __uint_as_float(ru[i] & 0xffff0000u) + round_bf16(sum[2 * i + 1]);
-        }
-      }
-      uint4 o4;
-      o4.x = (uint32_t)f32_to_bf16(sum[0]) | ((uint32_t)f32_to_bf16(sum[1]) << 16);
-      o4.y = (uint32_t)f32_to_bf16(sum[2]) | ((uint32_t)f32_to_bf16(sum[3]) << 16);
-      o4.z = (uint32_t)f32_to_bf16(sum[4]) | ((uint32_t)f32_to_bf16(sum[5]) << 16);
-      o4.w = (uint32_t)f32_to_bf16(sum[6]) | ((uint32_t)f32_to_bf16(sum[7]) << 16);
-      *(uint4*)(p.comb + (long)tt * p.N + c0) = o4;
-    }
+    handoff_combine<CG * WCOLS>(p.perm, p.topk, row0, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N, p.residual,
+                                p.comb, s_tok);
   }
 }
 

@@ -61,9 +61,10 @@ def bf16_block_m(pkg, T, H, I, E, k):
                                           (64, 2048, 768, 128, 8, 16), (200, 2048, 768, 128, 8, 128),
                                           (600, 2048, 768, 128, 8, 128), (37, 384, 256, 20, 5, 32),
                                           (100, 384, 256, 8, 2, 64), (257, 1024, 640, 12, 6, 128),
-                                          (600, 4096, 1536, 16, 8, 128), (40, 512, 256, 4, 2, 128)])
+                                          (600, 4096, 1536, 16, 8, 128), (40, 512, 256, 4, 2, 128),
+                                          (2, 384, 256, 20, 5, 16)])
 def test_bf16_block_matches_oracle(pkg, dev, T, H, I, E, k, bm):
-    """16-row tiles (S <= 8 E), above the 128-row LDS-tiled kernel; where H % 256 != 0, 32-row
+    """16-row tiles (S <= 8 E; from 2 tokens on the down GEMM combines each token itself), above the 128-row LDS-tiled kernel; where H % 256 != 0, 32-row
     tiles (S <= 16 E) and 64-row tiles.  128-row cases at the 30B and 235B widths, with 5 K blocks
     of 128 in the down GEMM's h (I = 640) and with the minimum of 4 bf16 K blocks (I = 256)."""
     assert bf16_block_m(pkg, T, H, I, E, k) == bm
