@@ -60,8 +60,12 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // SHA (32-row tiles, no K split): the tile's activation K block is staged once per workgroup in
 // LDS and every column wave reads its fragments there, instead of each wave loading the same
 // rows from memory (the four column waves would put 4x the activation bytes through L1).
+// The 16-row down GEMM is held to 80 VGPRs (6 waves per SIMD instead of 5, no spills): more
+// weight streams in flight (down at 8 / 32 / 64 tokens 25.7 / 42.4 / 47.2 -> 24.7 / 41.2 / 46.4
+// us).  The same bound on gate_up spills and runs slower (64 tokens 70 -> 119 us).
 template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
-__global__ __launch_bounds__(256) void grouped_gemm_fp8_kernel(GemmArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
+void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
   constexpr int NOP = MODE == MODE_GATE_UP ? 2 : DN;  // B operands per wave (gate, up | column slices)
   constexpr int BM = 16 * WM;
