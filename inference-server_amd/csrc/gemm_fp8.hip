@@ -62,7 +62,9 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // rows from memory (the four column waves would put 4x the activation bytes through L1).
 // The 16-row down GEMM is held to 80 VGPRs (6 waves per SIMD instead of 5, no spills): more
 // weight streams in flight (down at 8 / 32 / 64 tokens 25.7 / 42.4 / 47.2 -> 24.7 / 41.2 / 46.4
-// us).  The same bound on gate_up spills and runs slower (64 tokens 70 -> 119 us).
+// us).  The same bound on gate_up spills and runs slower (64 tokens 70 -> 119 us); with its loads
+// rewritten as a uniform base + 32-bit lane offsets it fits 80 VGPRs (2 spilled) but still runs
+// slower at 6 waves (64 tokens 69.5 -> 86.3 us).
 template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
