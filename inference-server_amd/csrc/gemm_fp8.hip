@@ -64,7 +64,8 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // weight streams in flight (down at 8 / 32 / 64 tokens 25.7 / 42.4 / 47.2 -> 24.7 / 41.2 / 46.4
 // us).  The same bound on gate_up spills and runs slower (64 tokens 70 -> 119 us); with its loads
 // rewritten as a uniform base + 32-bit lane offsets it fits 80 VGPRs (2 spilled) but still runs
-// slower at 6 waves (64 tokens 69.5 -> 86.3 us).
+// slower at 6 waves (64 tokens 69.5 -> 86.3 us), and capped at 4 or 3 workgroups per CU (LDS
+// padding) slower as well (72.7 / 80.1 us): 5 is gate_up's best occupancy.
 template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
