@@ -231,8 +231,9 @@ def run_config(pkg, torch, layer, T, steps, warmup, router, xs):
 
 
 def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
-    """Per-step time when every step replays a captured HIP graph (one graph per input /
-    weight-copy pair of the rotation): the small batches without host launch cost."""
+    """Per-step time when the steps replay a captured HIP graph: one graph holds a whole weight
+    rotation (one block call per weight copy, as a decode step's graph holds all its layers), so
+    the figure is the GPU's time per layer without host launch cost per call."""
     n_rot = layer.n_rot(T)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -241,22 +242,20 @@ def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
             pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, *layer.copies[j])
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    graphs = []
-    for j in range(n_rot):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for j in range(n_rot):
             pkg.moe_block_fp8(xs[j % len(xs)], router, K_TOP, *layer.copies[j])
-        graphs.append(g)
-    for g in graphs:
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
+    reps = max(1, math.ceil(steps / n_rot))
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     st.record()
-    for i in range(steps):
-        graphs[i % n_rot].replay()
+    for _ in range(reps):
+        g.replay()
     en.record()
     torch.cuda.synchronize()
-    return st.elapsed_time(en) / steps
+    return st.elapsed_time(en) / (reps * n_rot)
 
 
 def roofline_for(shape, T, slots, n_active):
