@@ -250,9 +250,9 @@ int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_norm_w, const 
  * Replaces Qwen3MoeDecoderLayer.forward's TF/models/qwen3_moe/modeling_qwen3_moe.py:341-347
  * (the residual add after the attention, post_attention_layernorm, the sparse block :276-281,
  * the residual add).  h_add is the attention's o_proj output; other arguments as
- * moe_mi355x_block_fp8.  Below 512 tokens the residual add, the RMSNorm, the router GEMM and the
- * x quantisation run in one launch (the router workgroups normalise the rows they read), with
- * the same bits as the separate RMSNorm.
+ * moe_mi355x_block_fp8.  The residual add and the RMSNorm run in one launch (which also writes
+ * h'), the router GEMM and the x quantisation in the next; the residual add after the block rides
+ * in the combine.
  */
 size_t moe_mi355x_moe_sublayer_workspace_bytes(int T, int H, int I, int E, int k);
 int moe_mi355x_moe_sublayer_fp8(const void* h, const void* h_add, const void* ln_weight, float eps,

@@ -17,8 +17,7 @@ int moe_launch_combine(const uint16_t* pairs, const void* ids, int id_bytes, con
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm, void* logits,
                      void* ids, int id_bytes, void* weights, void* workspace, size_t workspace_bytes, hipStream_t s,
                      uint8_t* xq, float* sx, int block_m, int32_t* perm, int32_t* counts, int32_t* offsets,
-                     int32_t* tiles, int32_t* n_tiles, int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt,
-                     const void* h_add, const void* ln_w, float eps, void* hs_out);
+                     int32_t* tiles, int32_t* n_tiles, int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt);
 int moe_launch_align_counted(const void* ids, int id_bytes, int S, int E, int block_m, const int32_t* bc,
                              int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
                              hipStream_t s, int32_t* zero, int nzero);
@@ -170,8 +169,7 @@ extern "C" int moe_mi355x_block_bf16(const void* x, const void* w_router, int T,
   const bool counted = !fused && w.align_ws_bytes > 0;
   int rc = moe_launch_route(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes, s,
                             nullptr, nullptr, w.block_m, fused ? w.perm : nullptr, w.counts, w.offsets, w.tiles,
-                            w.n_tiles, counted ? (int32_t*)w.align_ws : nullptr, w.cnt, w.n_cnt, nullptr, nullptr, 0.f,
-                            nullptr);
+                            w.n_tiles, counted ? (int32_t*)w.align_ws : nullptr, w.cnt, w.n_cnt);
   if (rc) return rc;
   if (counted) {
     rc = moe_launch_align_counted(id_out, idb, T * k, E, w.block_m, (const int32_t*)w.align_ws, w.perm, w.counts,

@@ -20,63 +20,18 @@ constexpr int kMaxKSplit = 16;      // router K-split partials summed by the top
 // k + 32 u + 8 g of row r for u = 0..3, i.e. the four lanes r, r+16, r+32, r+48 hold one
 // complete 128-column group; every wave forms the group amax and wave w quantises and
 // stores the values of u = w.
-//
-// NORM (the MoE sublayer's prologue, with xq): x is not given normalised.  The kernel reads the
-// residual stream h and the attention output h_add, forms hs = bf16(h + h_add) (h_add null: hs =
-// h), the RMSNorm row factor r = 1 / sqrt(mean(hs^2) + eps) of each of its 16 rows (every wave
-// sums whole rows in the lane order of rms_norm_kernel, so r is the same fp32 value), and feeds
-// x = bf16(w_ln * bf16(hs * r)) to the GEMM and the quantisation; the workgroups of expert block
-// 0 also write hs (the residual of the block's combine) for their K chunk.
-// (Qwen3MoeDecoderLayer.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:341-346: the residual
-// add, post_attention_layernorm :294-299, and the router of the sparse block.)
-template <bool NORM>
 __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wr, int T, int H,
                                                           int E, int kchunk, float* __restrict__ part,
                                                           uint8_t* __restrict__ xq, float* __restrict__ sx,
-                                                          int32_t* __restrict__ zero, int nzero,
-                                                          const uint16_t* __restrict__ h_add,
-                                                          const uint16_t* __restrict__ ln_w, float eps,
-                                                          uint16_t* __restrict__ hs_out) {
-  // the reference's separate bf16 ops: no multiply-add contraction across their roundings
+                                                          int32_t* __restrict__ zero, int nzero) {
+  // the quantisation's fp32 steps stay separate operations (no multiply-add contraction)
 #pragma clang fp contract(off)
   // workgroup 0 clears the expert sort's chunk histograms that the top-k kernel fills next
   if (zero != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
     for (int i = threadIdx.x; i < nzero; i += blockDim.x) zero[i] = 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t0 = blockIdx.x * kRouterTileT;
-  __shared__ float s_r[kRouterTileT];
-  if constexpr (NORM) {
-    // r of rows t0 .. t0 + 15, four per wave: lane l sums chunks c = (64 i + l) * 8 in order
-    for (int rr = wave; rr < kRouterTileT; rr += 4) {
-      const int row = min(t0 + rr, T - 1);
-      float ss = 0.f;
-      for (int c = lane * 8; c < H; c += 512) {
-        const uint4 hv = *(const uint4*)(x + (long)row * H + c);
-        uint32_t u[4] = {hv.x, hv.y, hv.z, hv.w};
-        if (h_add != nullptr) {
-          const uint4 av = *(const uint4*)(h_add + (long)row * H + c);
-          const uint32_t au[4] = {av.x, av.y, av.z, av.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float lo = __uint_as_float(u[j] << 16) + __uint_as_float(au[j] << 16);
-            const float hi = __uint_as_float(u[j] & 0xffff0000u) + __uint_as_float(au[j] & 0xffff0000u);
-            u[j] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = __uint_as_float(u[j] << 16), b = __uint_as_float(u[j] & 0xffff0000u);
-          ss = fmaf(a, a, ss);
-          ss = fmaf(b, b, ss);
-        }
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) s_r[rr] = 1.0f / sqrtf(ss / (float)H + eps);
-    }
-    __syncthreads();
-  }
-  const float row_r = NORM ? s_r[lane & 15] : 1.0f;
   const int kbeg = blockIdx.z * kchunk;
   const int kend = min(H, kbeg + kchunk);
   const bool quant = xq != nullptr && blockIdx.y == 0;  // workgroup-uniform
@@ -85,55 +40,21 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
   const int re = min(e0 + (lane & 15), E - 1);
   const int kq = (lane >> 4) * 8;
   const uint16_t* xa = x + (long)rt * H + kq;
-  const uint16_t* da = NORM && h_add != nullptr ? h_add + (long)rt * H + kq : nullptr;
   const uint16_t* wb = wr + (long)re * H + kq;
   const bool row_ok = t0 + (lane & 15) < T;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   const int n128 = (kend - kbeg) >> 7;  // whole 128-wide chunks
   v8bf a0[4], b0[4], a1[4], b1[4];
-  uint4 d0[4], d1[4];  // NORM: h_add at the positions of a0 / a1 (the raw h)
-  // NORM: turn the raw h of chunk kk_ in A_ (h_add in D_) into the normalised x, in place;
-  // the expert-block-0 workgroups write hs (wave w: the values of u = w)
-#define ROUTER_NORM(A_, D_, kk_)                                                                  \
-  do {                                                                                            \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                               \
-      uint4 hv_ = __builtin_bit_cast(uint4, A_[u]);                                               \
-      uint32_t hu_[4] = {hv_.x, hv_.y, hv_.z, hv_.w};                                             \
-      if (h_add != nullptr) {                                                                     \
-        const uint32_t au_[4] = {D_[u].x, D_[u].y, D_[u].z, D_[u].w};                             \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                           \
-          const float lo_ = __uint_as_float(hu_[j] << 16) + __uint_as_float(au_[j] << 16);        \
-          const float hi_ = __uint_as_float(hu_[j] & 0xffff0000u) + __uint_as_float(au_[j] & 0xffff0000u); \
-          hu_[j] = (uint32_t)f32_to_bf16(lo_) | ((uint32_t)f32_to_bf16(hi_) << 16);               \
-        }                                                                                         \
-        if (quant && u == wave && row_ok)                                                         \
-          *(uint4*)(hs_out + (long)(t0 + (lane & 15)) * H + (kk_) + 32 * u + kq) =                \
-              make_uint4(hu_[0], hu_[1], hu_[2], hu_[3]);                                         \
-      }                                                                                           \
-      const uint4 wv_ = *(const uint4*)(ln_w + (kk_) + 32 * u + kq);                              \
-      const uint32_t wu_[4] = {wv_.x, wv_.y, wv_.z, wv_.w};                                       \
-      uint32_t o_[4];                                                                             \
-      _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                             \
-        const float a_ = round_bf16(__uint_as_float(hu_[j] << 16) * row_r);                       \
-        const float b_ = round_bf16(__uint_as_float(hu_[j] & 0xffff0000u) * row_r);               \
-        o_[j] = (uint32_t)f32_to_bf16(__uint_as_float(wu_[j] << 16) * a_) |                       \
-                ((uint32_t)f32_to_bf16(__uint_as_float(wu_[j] & 0xffff0000u) * b_) << 16);        \
-      }                                                                                           \
-      A_[u] = __builtin_bit_cast(v8bf, make_uint4(o_[0], o_[1], o_[2], o_[3]));                   \
-    }                                                                                             \
-  } while (0)
   // MFMAs of chunk c_ on (A_, B_) after issuing the loads of chunk c_ + 1 (clamped: the
   // last chunk reloads itself) into (AN_, BN_), then the x quantisation of chunk c_
-#define ROUTER_STEP(A_, B_, AN_, BN_, D_, DN_, c_)                                                \
+#define ROUTER_STEP(A_, B_, AN_, BN_, c_)                                                         \
   do {                                                                                            \
     const int kk_ = kbeg + 128 * (c_);                                                            \
     const int nx_ = kbeg + 128 * min((c_) + 1, n128 - 1);                                         \
     _Pragma("unroll") for (int u = 0; u < 4; ++u) {                                               \
       AN_[u] = *(const v8bf*)(xa + nx_ + 32 * u);                                                 \
       BN_[u] = *(const v8bf*)(wb + nx_ + 32 * u);                                                 \
-      if (NORM && h_add != nullptr) DN_[u] = *(const uint4*)(da + nx_ + 32 * u);                  \
     }                                                                                             \
-    if constexpr (NORM) ROUTER_NORM(A_, D_, kk_);                                                 \
     _Pragma("unroll") for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A_[u], B_[u], acc, 0, 0, 0); \
     if (quant) {                                                                                  \
       /* the e4m3 rule of quant_group16: s = amax / 448 (1 if 0), q = e4m3(clamp(x / s)) */      \
@@ -161,15 +82,13 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
     for (int u = 0; u < 4; ++u) {
       a0[u] = *(const v8bf*)(xa + kbeg + 32 * u);
       b0[u] = *(const v8bf*)(wb + kbeg + 32 * u);
-      if (NORM && h_add != nullptr) d0[u] = *(const uint4*)(da + kbeg + 32 * u);
     }
   }
   for (int c = 0; c < n128; c += 2) {
-    ROUTER_STEP(a0, b0, a1, b1, d0, d1, c);
-    if (c + 1 < n128) ROUTER_STEP(a1, b1, a0, b0, d1, d0, c + 1);
+    ROUTER_STEP(a0, b0, a1, b1, c);
+    if (c + 1 < n128) ROUTER_STEP(a1, b1, a0, b0, c + 1);
   }
 #undef ROUTER_STEP
-#undef ROUTER_NORM
   int k = kbeg + 128 * n128;
   for (; k < kend; k += 32) {
     v8bf a = *(const v8bf*)(xa + k), b = *(const v8bf*)(wb + k);
@@ -526,9 +445,6 @@ int moe_route_numerics_key(int T, int H, int E, bool quant) {
   return (tiled ? 1 << 16 : 0) | kchunk;
 }
 
-// Whether the router GEMM can take the RMSNorm prologue (its small-batch kernel; H % 128 == 0).
-bool moe_route_can_norm(int T, int H) { return !route_tiled(T, H) && H % MOE_GROUP == 0; }
-
 // Whether moe_launch_route can run the top-k and the expert sort as one workgroup.
 bool moe_route_can_fuse_align(int T, int E, int k) {
   // one workgroup routes every token, so the whole top-k runs on one CU: a win over the
@@ -543,11 +459,8 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
                      int32_t* perm, int32_t* counts, int32_t* offsets, int32_t* tiles, int32_t* n_tiles,
-                     int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt, const void* h_add,
-                     const void* ln_w, float eps, void* hs_out) {
+                     int32_t* chunk_counts, int32_t* gemm_cnt, int n_gemm_cnt) {
   if (T == 0) return MOE_OK;
-  // the normalising prologue (ln_w): small batches only, and it always quantises x
-  MOE_RETURN_IF(ln_w != nullptr && (!moe_route_can_norm(T, H) || xq == nullptr), MOE_ERR_INVALID_ARG);
   const bool quant = xq != nullptr;
   MOE_RETURN_IF(chunk_counts != nullptr && perm != nullptr, MOE_ERR_INVALID_ARG);
   const int nzero = chunk_counts ? (int)(((long)T * k + kChunk - 1) / kChunk) * (E + 1) : 0;
@@ -565,14 +478,8 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
                (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
   } else {
     dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
-    if (ln_w != nullptr)
-      MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel<true>, g1, dim3(256), 0, s, (const uint16_t*)x,
-                 (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero,
-                 (const uint16_t*)h_add, (const uint16_t*)ln_w, eps, (uint16_t*)hs_out);
-    else
-      MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel<false>, g1, dim3(256), 0, s, (const uint16_t*)x,
-                 (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero,
-                 (const uint16_t*)nullptr, (const uint16_t*)nullptr, 0.f, (uint16_t*)nullptr);
+    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
   }
   MOE_CHECK_LAUNCH();
   if (perm != nullptr) {
@@ -597,7 +504,7 @@ extern "C" int moe_mi355x_route(const void* x, const void* w_router, int T, int 
   MOE_RETURN_IF(!moe_aligned16(x) || !moe_aligned16(w_router), MOE_ERR_ALIGNMENT);
   return moe_launch_route(x, w_router, T, H, E, k, renorm, logits, ids, id_bytes, weights, workspace,
                           workspace_bytes, (hipStream_t)stream, nullptr, nullptr, 0, nullptr, nullptr, nullptr,
-                          nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0.f, nullptr);
+                          nullptr, nullptr, nullptr, nullptr, 0);
 }
 
 extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, int renorm, void* ids,

@@ -135,8 +135,8 @@ def test_moe_sublayer_with_attention_residual(pkg, dev, T):
 
 @pytest.mark.parametrize("T", [1, 8, 64, 128])
 def test_moe_sublayer_prologue_matches_oracle(pkg, dev, T):
-    """The MoE sublayer at the Qwen3-30B-A3B shape, whose residual add, post-attention RMSNorm,
-    router GEMM and x quantisation run in one launch for decode batches, against the oracle:
+    """The MoE sublayer at the Qwen3-30B-A3B shape (residual add + post-attention RMSNorm in one
+    launch, router GEMM + x quantisation in the next) against the oracle:
     hs = bf16(h + o), x = attn_oracle.rms_norm(hs, w_ln), moe_oracle's router and FP8 experts
     on x, then bf16(hs + block).  Tokens whose oracle logits have a near-tie at the top-k
     boundary (the 8th and 9th logits within 1 bf16 ulp) are left out: one ulp of RMSNorm or
