@@ -16,10 +16,12 @@ contexts uniform in [512, 8192] (page size 16), o_proj, RMSNorm and the FP8 MoE 
 replayed as one HIP graph; it reports decode tokens/s and the per-layer MoE and attention shares.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--tokens 64] [--zipf] [--no-sweep]
-                       [--no-cpu] [--no-decode-step] [--decode-step-only] [--copy-probe] [--shape 30b|235b]
+                       [--no-cpu] [--no-decode-step] [--decode-step-only] [--copy-probe] [--library-probe] [--shape 30b|235b]
   --zipf        apply the calibrated Zipf(s=1.1) router bias to the headline batch (config 3)
   --copy-probe  first run a plain 256 MiB device copy three times: the reference kernel whose
                 FETCH_SIZE / WRITE_SIZE counters calibrate the traffic measurement
+  --library-probe  time the vendor's dense FP8 / bf16 GEMMs on the expert GEMM shapes (a ceiling
+                reference for the grouped kernels) and exit
   --shape 235b  the headline line on the Qwen3-235B-A22B layer instead (with --no-sweep, for profiling)
 """
 
@@ -468,6 +470,57 @@ def decode_step_entry(pkg, torch, dev, steps=10, n_layers=48, batch=128, seed=0)
     return entry
 
 
+def library_probe(torch, dev, reps=50):
+    """The library's dense GEMMs on the expert GEMMs' shapes: ``torch._scaled_mm`` (FP8 e4m3 x e4m3,
+    one fp32 scale per tensor, bf16 out) and the bf16 matmul, both hipBLASLt on this build, with
+    HIP events on torch's current stream (where the library launches).  Rows are token-expert
+    pairs: all 32768 pairs of the 4096-token prefill chunk as one dense GEMM (no grouping, no block
+    scales, no gather, no fused SiLU or quantisation: an upper bound for what a grouped kernel of
+    the same shape can reach), one hot expert's rows (3222 under the Zipf routing), one cold
+    expert's (139), and the library's best case 8192^3."""
+    shapes = [("gate_up, all pairs", 32768, 1536, 2048), ("down, all pairs", 32768, 2048, 768),
+              ("gate_up, hot expert", 3222, 1536, 2048), ("gate_up, cold expert", 139, 1536, 2048),
+              ("square", 8192, 8192, 8192)]
+    out = []
+    for name, M, N, K in shapes:
+        a = torch.randn((M, K), device=dev).to(torch.float8_e4m3fn)
+        b = torch.randn((N, K), device=dev).to(torch.float8_e4m3fn)
+        one = torch.ones((), device=dev)
+        ab, bb = torch.randn((M, K), device=dev, dtype=torch.bfloat16), torch.randn((N, K), device=dev, dtype=torch.bfloat16)
+        fns = {"fp8": (lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16), 5000.0),
+               "bf16": (lambda: ab @ bb.t(), 2500.0)}
+        entry = {"gemm": name, "M": M, "N": N, "K": K}
+        for dt, (fn, peak) in fns.items():
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            entry[dt] = {"us": round(us, 2), "tflops": round(tf, 1), "peak_frac": round(tf / peak, 4)}
+        out.append(entry)
+        del a, b, ab, bb
+    # the floor of one dependent launch: back-to-back tiny elementwise kernels on one stream
+    t = torch.zeros(64, device=dev)
+    for _ in range(10):
+        t.add_(1.0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(1000):
+        t.add_(1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    out.append({"gemm": "none: one tiny elementwise kernel per launch, 1000 back to back",
+                "us_per_launch": round(e0.elapsed_time(e1) * 1e3 / 1000, 2)})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -478,6 +531,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--zipf", action="store_true")
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--library-probe", action="store_true",
+                    help="time the vendor GEMMs (hipBLASLt through torch) on dense shapes of the expert "
+                         "GEMMs, as a ceiling reference for the grouped kernels; prints one JSON object")
     ap.add_argument("--no-decode-step", action="store_true", help="skip the 48-layer decode step (config 5)")
     ap.add_argument("--decode-step-only", action="store_true", help="run only the 48-layer decode step")
     ap.add_argument("--shape", choices=["30b", "235b"], default="30b",
@@ -508,6 +564,9 @@ def main():
         del src, dst
     if args.decode_step_only:
         print(json.dumps({"decode_step": decode_step_entry(pkg, torch, dev)}), flush=True)
+        return
+    if args.library_probe:
+        print(json.dumps({"library_probe": library_probe(torch, dev)}), flush=True)
         return
     if args.experts_dtype == "bf16":
         g = torch.Generator(device=dev).manual_seed(0)
