@@ -21,7 +21,7 @@
 // and WM 16-row M fragments of one expert tile.  K-split partials are summed
 // through LDS in a fixed order (deterministic).  Each weight byte is read once
 // per M tile, straight from HBM into VGPRs: the decode case is a weight stream.
-#include "common.h"
+#include "route_dev.h"
 
 namespace {
 
@@ -51,6 +51,18 @@ struct GemmArgs {
   int32_t* tok_cnt;
   uint16_t* comb;
   const uint16_t* residual;  // down: comb = bf16(residual + bf16(sum)) when non-null
+  // ROUTED gate_up (single-token decode): tile y is routing slot y = t * topk + j, one row, and
+  // the workgroup routes token t itself from the router GEMM's K-split partials; the workgroups
+  // of column block 0 write the routing outputs and the one-row tile list the down GEMM reads.
+  const float* part;  // [ksplit, T, E] fp32
+  int ksplit, T, E, renorm;
+  uint16_t* logits;   // bf16 [T, E] or null
+  void* ids;          // [T, topk], int32 or int64 (id_bytes)
+  int id_bytes;
+  uint16_t* wts;      // bf16 [T, topk]
+  int32_t* perm_out;  // [S]: identity (slot y holds pair y)
+  int32_t* tiles_out; // [S, 4]: {expert, y, 1, 0}
+  int32_t* n_tiles_out;
 };
 
 constexpr int kMaxKB = 32;  // K <= 4096
@@ -66,19 +78,42 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // rewritten as a uniform base + 32-bit lane offsets it fits 80 VGPRs (2 spilled) but still runs
 // slower at 6 waves (64 tokens 69.5 -> 86.3 us), and capped at 4 or 3 workgroups per CU (LDS
 // padding) slower as well (72.7 / 80.1 us): 5 is gate_up's best occupancy.
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
   constexpr int NOP = MODE == MODE_GATE_UP ? 2 : DN;  // B operands per wave (gate, up | column slices)
   constexpr int BM = 16 * WM;
 
+  static_assert(!ROUTED || (MODE == MODE_GATE_UP && WM == 1 && !SHA), "routed slots are one-row gate_up tiles");
   const int tile = blockIdx.y;
-  if (tile >= p.n_tiles[0]) return;  // workgroup-uniform
-  const int4 ti = *(const int4*)(p.tiles + 4 * tile);
-  const int e = ti.x, row0 = ti.y, rows = ti.z;
-
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int e, row0, rows;
+  if constexpr (ROUTED) {
+    // every wave routes the slot's token (the same bits in each: route_token is deterministic);
+    // lane j < topk holds slot j's expert and weight
+    const int t = tile / p.topk, j = tile - t * p.topk;
+    const bool writer = blockIdx.x == 0 && j == 0 && wave == 0;  // one wave per token
+    int my_e;
+    float my_w;
+    route_token(p.part, p.ksplit, nullptr, p.T, p.E, p.topk, p.renorm, writer ? p.logits : nullptr, t, my_e, my_w);
+    e = __builtin_amdgcn_readlane(my_e, j);
+    row0 = tile;
+    rows = 1;
+    if (writer && lane < p.topk) store_route(p.ids, p.id_bytes, p.wts, (long)t * p.topk + lane, my_e, my_w);
+    if (blockIdx.x == 0 && wave == 0 && lane == 0) {
+      *(int4*)(p.tiles_out + 4 * tile) = make_int4(e, tile, 1, 0);
+      p.perm_out[tile] = tile;
+      if (tile == 0) p.n_tiles_out[0] = gridDim.y;
+    }
+  } else {
+    if (tile >= p.n_tiles[0]) return;  // workgroup-uniform
+    const int4 ti = *(const int4*)(p.tiles + 4 * tile);
+    e = ti.x;
+    row0 = ti.y;
+    rows = ti.z;
+  }
+
   const int cg = wave % CG, ks = wave / CG;
   const int lr = lane & 15, lg = lane >> 4;
   const int KB = p.K / MOE_GROUP;
@@ -118,7 +153,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 
   for (int r = threadIdx.x; r < BM; r += blockDim.x) {
     const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
-    s_arow[r] = MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
+    s_arow[r] = ROUTED ? tile / p.topk : MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
@@ -335,7 +370,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
 }
 
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false>
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;
@@ -343,7 +378,7 @@ int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   // come after every working one instead of between them, and consecutive workgroups stream
   // adjacent weight rows of one expert (gate_up at 64 tokens 75 -> 70 us)
   dim3 grid(a.N / (WCOLS * CG), max_tiles);
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA>),
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED>),
              grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -416,4 +451,25 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   else
     rc = launch_gemm<MODE_DOWN, 4, 1>(g2, max_tiles, s);
   return rc;
+}
+
+// Single-token decode (one row per routing slot, S = T * k <= 2 E): gate_up routes its own slot
+// from the router GEMM's K-split partials (no top-k or sort launch) and writes the routing
+// outputs, the identity slot order and the one-row tile list; then the down GEMM of the 16-row
+// tiles with the in-launch h quantisation and token combine (tile_cnt and tok_cnt zero on entry).
+// Every expert GEMM row is computed as on the sorted path, so the bits are the same.
+int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                                    const uint8_t* w2, const float* s2, const float* part, int ksplit, int T, int E,
+                                    int renorm, uint16_t* logits, void* ids, int id_bytes, uint16_t* wts,
+                                    int32_t* perm, int32_t* tiles, int32_t* n_tiles, uint16_t* h, uint8_t* hq,
+                                    float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s, int32_t* tile_cnt,
+                                    int32_t* tok_cnt, uint16_t* comb, const uint16_t* residual) {
+  const int S = T * k;
+  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh, nullptr, nullptr,
+              nullptr, part, ksplit, T, E, renorm, logits, ids, id_bytes, wts, perm, tiles, n_tiles};
+  int rc = launch_gemm<MODE_GATE_UP, 1, 4, 1, false, true>(g1, S, s);
+  if (rc) return rc;
+  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, wts, pairs, I, H, k, nullptr, nullptr, nullptr,
+              tok_cnt, comb, residual};
+  return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, S, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, S, s);
 }

@@ -16,6 +16,16 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
                              uint8_t* hq, float* sh, uint16_t* pairs, int S, int H, int I, int k,
                              int block_m, hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
                              const uint16_t* residual);
+bool route_tiled_host(int T, int H);
+int moe_launch_router_gemm(const void* x, const void* w_router, int T, int H, int E, void* workspace,
+                           size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int32_t* zero, int nzero,
+                           int* ks_eff_out);
+int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                                    const uint8_t* w2, const float* s2, const float* part, int ksplit, int T, int E,
+                                    int renorm, uint16_t* logits, void* ids, int id_bytes, uint16_t* wts,
+                                    int32_t* perm, int32_t* tiles, int32_t* n_tiles, uint16_t* h, uint8_t* hq,
+                                    float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s, int32_t* tile_cnt,
+                                    int32_t* tok_cnt, uint16_t* comb, const uint16_t* residual);
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
@@ -284,6 +294,16 @@ extern "C" size_t moe_mi355x_block_workspace_bytes(int T, int H, int I, int E, i
 }
 
 namespace {
+// Batches of up to 4 tokens skip the top-k + sort launch: every routing slot is its own one-row
+// tile and the gate_up GEMM routes it (the bits of the sorted path).  Two slots that name one
+// expert then stream its weights twice, which costs more than the launch saves from 5 tokens on
+// (Qwen3-30B-A3B layer: 1 / 2 / 4 tokens 31.7 / 38.1 / 50.8 -> 28.9 / 34.8 / 49.4 us; 5 / 8 tokens
+// 54.2 / 68.3 -> 56.1 / 75.6 us).
+constexpr int kRoutedMaxTokens = 4;
+bool routed_path(int T, int H, int E, int k, int block_m) {
+  return T <= kRoutedMaxTokens && block_m == 16 && T * k <= 2 * E && E <= 256 && !route_tiled_host(T, H);
+}
+
 // Router + experts; `residual` non-null adds it in the combine (moe_mi355x_moe_sublayer_fp8).
 int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, int k, int renorm, const void* w13,
                const float* s13, const void* w2, const float* s2, void* out, void* logits, void* ids, int id_bytes,
@@ -293,6 +313,18 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
   const int idb = ids ? id_bytes : 4;
   void* wt = weights ? weights : (void*)b.weights;
   const ExpertsWs w = carve_experts(b.experts_ws, T, H, I, E, k);
+  if (routed_path(T, H, E, k, w.block_m)) {
+    // router GEMM (clearing the GEMMs' hand-off counters), then gate_up routing its own slots
+    int ks_eff = 0;
+    int rc = moe_launch_router_gemm(x, w_router, T, H, E, b.route_ws, b.route_bytes, s, w.xq, w.sx, w.cnt, w.n_cnt,
+                                    &ks_eff);
+    if (rc) return rc;
+    return moe_launch_grouped_gemms_routed(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2,
+                                           (const float*)b.route_ws, ks_eff, T, E, renorm, (uint16_t*)lg, id_out, idb,
+                                           (uint16_t*)wt, w.perm, w.tiles, w.n_tiles, w.h, w.hq, w.sh, w.pairs, H, I,
+                                           k, s, w.cnt, w.cnt + (long)w.max_tiles * (I / MOE_GROUP), (uint16_t*)out,
+                                           (const uint16_t*)residual);
+  }
   // decode batches: x quantisation rides in the router GEMM, align in the top-k kernel; large
   // batches: the top-k kernel fills the expert sort's chunk histograms (cleared by the router
   // GEMM), and one launch finishes the sort

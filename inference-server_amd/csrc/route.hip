@@ -3,13 +3,13 @@
 //
 // Reference: Qwen3MoeTopKRouter.forward, TF/models/qwen3_moe/modeling_qwen3_moe.py:258-267.
 #include "align_dev.h"
+#include "route_dev.h"
 
 namespace {
 
 constexpr int kRouterTileT = 16;    // tokens per MFMA tile
 constexpr int kRouterWaveE = 16;    // experts per wave
 constexpr int kRouterBlockE = 64;   // experts per workgroup (4 waves)
-constexpr int kMaxKSplit = 16;      // router K-split partials summed by the top-k kernel
 
 // partial[z, t, e] = sum over k in chunk z of x[t, k] * w[e, k]   (fp32)
 // grid (ceil(T/16), ceil(E/64), ksplit), block 256: wave w computes tokens t0..t0+15 x
@@ -220,101 +220,6 @@ __global__ __launch_bounds__(256) void router_gemm_tiled_kernel(const uint16_t* 
   }
 }
 
-// bf16 bit pattern -> unsigned key that orders like the value (-0 folded onto +0).
-__device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
-  if (b == 0x8000u) b = 0;
-  return (b & 0x8000u) ? (uint32_t)(~b & 0xffffu) : (uint32_t)(b | 0x8000u);
-}
-
-// Routing of one token by one wave.  Each lane holds experts lane, lane+64, lane+128,
-// lane+192.  Either sums the router's K-split partials (part != nullptr) and writes the
-// bf16 logits, or reads given logits.  Lane j < k returns the j-th expert (descending
-// logit, ties to the lower id) and its (renormalised) weight before the bf16 cast.
-__device__ __forceinline__ void route_token(const float* __restrict__ part, int ksplit,
-                                            const uint16_t* __restrict__ logits_in, int T, int E, int k,
-                                            int renorm, uint16_t* __restrict__ logits_out, int t, int& my_e,
-                                            float& my_w) {
-  const int lane = threadIdx.x & 63;
-  uint16_t lb[4];
-  bool valid[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int e = lane + 64 * c;
-    valid[c] = e < E;
-    lb[c] = 0;
-    if (!valid[c]) continue;
-    if (part) {
-      // all partial loads issue before the first add: they are independent, and a
-      // load-add chain would pay the cross-XCD load latency ksplit times
-      // (unconditional loads of a clamped slab index: a guarded load would compile to a
-      // branch and a wait per partial)
-      float pv[kMaxKSplit];
-#pragma unroll
-      for (int z = 0; z < kMaxKSplit; ++z) pv[z] = part[((long)min(z, ksplit - 1) * T + t) * E + e];
-      float s = 0.f;
-#pragma unroll
-      for (int z = 0; z < kMaxKSplit; ++z) s += z < ksplit ? pv[z] : 0.f;
-      lb[c] = f32_to_bf16(s);
-      if (logits_out) logits_out[(long)t * E + e] = lb[c];
-    } else {
-      lb[c] = logits_in[(long)t * E + e];
-    }
-  }
-  // softmax in fp32 (modeling_qwen3_moe.py:261)
-  float m = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    if (valid[c]) m = fmaxf(m, bf16_to_f32(lb[c]));
-  m = wave_max_uniform(m);
-  float ex[4];
-  float zsum = 0.f;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    ex[c] = valid[c] ? expf(bf16_to_f32(lb[c]) - m) : 0.f;
-    zsum += ex[c];
-  }
-  zsum = wave_sum_uniform(zsum);
-  uint32_t key[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    key[c] = valid[c] ? ((bf16_order_key(lb[c]) << 16) | (0xffffu - (uint32_t)(lane + 64 * c))) : 0u;
-  // top-k: k rounds of wave arg-max on (logit, -id)   (modeling_qwen3_moe.py:262)
-  my_e = 0;
-  float my_p = 0.f, psum = 0.f;
-  for (int j = 0; j < k; ++j) {
-    uint32_t best = key[0];
-#pragma unroll
-    for (int c = 1; c < 4; ++c) best = key[c] > best ? key[c] : best;
-    best = wave_max_u32_uniform(best);
-    const int ew = (int)(0xffffu - (best & 0xffffu));
-    const int owner = ew & 63, slot = ew >> 6;
-    float pv = 0.f;
-    if (lane == owner) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (c == slot) {
-          pv = ex[c] / zsum;
-          key[c] = 0u;
-        }
-    }
-    pv = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(pv), owner));
-    psum += pv;  // sequential fp32 sum in top-k order, identical in every lane
-    if (lane == j) {
-      my_e = ew;
-      my_p = pv;
-    }
-  }
-  my_w = renorm ? my_p / psum : my_p;  // modeling_qwen3_moe.py:263-266
-}
-
-__device__ __forceinline__ void store_route(void* ids, int id_bytes, uint16_t* weights, long idx, int e, float w) {
-  weights[idx] = f32_to_bf16(w);
-  if (id_bytes == 8)
-    ((int64_t*)ids)[idx] = e;
-  else
-    ((int32_t*)ids)[idx] = e;
-}
-
 // One wave per token, 4 tokens per workgroup.  With `bc` (zeroed beforehand) each routed pair
 // also counts into its 1024-pair chunk's expert histogram bc[chunk][e], the first pass of the
 // expert sort (integer atomics: the counts do not depend on their order).
@@ -429,6 +334,8 @@ bool route_args_ok(int T, int H, int E, int k, int id_bytes) {
 
 }  // namespace
 
+bool route_tiled_host(int T, int H) { return route_tiled(T, H); }
+
 extern "C" size_t moe_mi355x_route_workspace_bytes(int T, int H, int E) {
   if (T <= 0 || H <= 0 || E <= 0) return 0;
   const int ks = route_ksplit(T, H, E);
@@ -452,6 +359,32 @@ bool moe_route_can_fuse_align(int T, int E, int k) {
   return T <= 16 && (long)T * E <= kFusedMaxLogits && (long)T * k <= kSingleMaxS;
 }
 
+// Router GEMM alone: fp32 K-split partials [ks_eff, T, E] in the workspace (ks_eff returned),
+// with xq/sx the x quantisation, with `zero` the nzero ints there cleared by workgroup 0.
+int moe_launch_router_gemm(const void* x, const void* w_router, int T, int H, int E, void* workspace,
+                           size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int32_t* zero, int nzero,
+                           int* ks_eff_out) {
+  const bool quant = xq != nullptr;
+  const int ks = route_ksplit(T, H, E);
+  const bool tiled = route_tiled(T, H);
+  const int kchunk = route_kchunk(H, ks, quant || tiled);
+  const int ks_eff = (H + kchunk - 1) / kchunk;  // <= ks: the workspace holds ks partial slabs
+  MOE_RETURN_IF(workspace_bytes < moe_mi355x_route_workspace_bytes(T, H, E) || !workspace, MOE_ERR_WORKSPACE);
+  float* part = (float*)workspace;
+  if (tiled) {
+    dim3 g1((T + kRtT - 1) / kRtT, (E + kRtE - 1) / kRtE, ks_eff);
+    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_tiled_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, zero, nzero);
+  } else {
+    dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
+    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
+               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, zero, nzero);
+  }
+  MOE_CHECK_LAUNCH();
+  *ks_eff_out = ks_eff;
+  return MOE_OK;
+}
+
 // Router GEMM and top-k softmax.  With xq/sx the router workgroups also quantise x
 // (needs H % 128 == 0).  With perm != nullptr (moe_route_can_fuse_align) the top-k and the expert
 // sort run fused in one workgroup and write the align outputs too.
@@ -466,22 +399,11 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   const int nzero = chunk_counts ? (int)(((long)T * k + kChunk - 1) / kChunk) * (E + 1) : 0;
   MOE_RETURN_IF(quant && H % MOE_GROUP, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(perm != nullptr && !moe_route_can_fuse_align(T, E, k), MOE_ERR_INVALID_ARG);
-  const int ks = route_ksplit(T, H, E);
-  const bool tiled = route_tiled(T, H);
-  const int kchunk = route_kchunk(H, ks, quant || tiled);
-  const int ks_eff = (H + kchunk - 1) / kchunk;  // <= ks: the workspace holds ks partial slabs
-  MOE_RETURN_IF(workspace_bytes < moe_mi355x_route_workspace_bytes(T, H, E) || !workspace, MOE_ERR_WORKSPACE);
+  int ks_eff = 0;
+  int rc = moe_launch_router_gemm(x, w_router, T, H, E, workspace, workspace_bytes, s, xq, sx, chunk_counts, nzero,
+                                  &ks_eff);
+  if (rc) return rc;
   float* part = (float*)workspace;
-  if (tiled) {
-    dim3 g1((T + kRtT - 1) / kRtT, (E + kRtE - 1) / kRtE, ks_eff);
-    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_tiled_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
-               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
-  } else {
-    dim3 g1((T + kRouterTileT - 1) / kRouterTileT, (E + kRouterBlockE - 1) / kRouterBlockE, ks_eff);
-    MOE_LAUNCH(MOE_PROF_ROUTER_GEMM, s, router_gemm_kernel, g1, dim3(256), 0, s, (const uint16_t*)x,
-               (const uint16_t*)w_router, T, H, E, kchunk, part, xq, sx, chunk_counts, nzero);
-  }
-  MOE_CHECK_LAUNCH();
   if (perm != nullptr) {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_align_kernel, dim3(1), dim3(kChunk), 0, s, part, ks_eff, T, E, k, renorm,
                (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights, block_m, perm, counts, offsets, tiles,

@@ -255,10 +255,10 @@ def router30b(dev):
     return (torch.randn((128, 2048), generator=g, device=dev) * 0.02).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("T", [1, 8, 16, 17, 64, 600])
+@pytest.mark.parametrize("T", [1, 3, 4, 5, 8, 16, 17, 64, 600])
 def test_block_30b_routing_paths(pkg, dev, w30b, router30b, T):
-    """Block forward across the routing variants: top-k + sort fused in one workgroup
-    (T <= 16), separate top-k then single-workgroup sort (T*k <= 4096), and the
+    """Block forward across the routing variants: routing inside the gate_up GEMM (T <= 4),
+    top-k + sort fused in one workgroup (T <= 16), separate top-k then single-workgroup sort (T*k <= 4096), and the
     multi-block sort."""
     rng = np.random.default_rng(30 + T)
     x = orc.gen_normal_bf16(rng, (T, 2048))
@@ -298,11 +298,12 @@ def test_sentinel_pairs_contribute_zero(pkg, dev, w30b, T):
     assert torch.equal(out, ref)
 
 
-@pytest.mark.parametrize("T", [8, 64, 600, 1024])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8, 64, 600, 1024])
 def test_block_fused_quant_is_bit_exact(pkg, dev, w30b, router30b, T):
     """The block path quantises x inside the router GEMM; the experts path quantises it in
     its own kernel.  Fed the block's routing, the experts path must reproduce the block's
-    output bit for bit (same e4m3 codes and scales, same deterministic GEMMs)."""
+    output bit for bit (same e4m3 codes and scales, same deterministic GEMMs).  Up to 4 tokens
+    the block's gate_up routes its own one-row slots with no sort; the experts path sorts."""
     rng = np.random.default_rng(70 + T)
     x = to_bf16(orc.gen_normal_bf16(rng, (T, 2048)), dev)
     out, (_, w, ids) = pkg.moe_block_fp8(x, router30b, 8, *w30b, return_routing=True)
