@@ -194,21 +194,21 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 
 // The token combine of a down-GEMM workgroup on the hand-off path, run by its last result wave
-// once the workgroup's pair rows (columns [bx CB, (bx + 1) CB) of its tile's rows) are stored
-// device-scope: one tile row (pair) per lane counts in for its token's column block in tok_cnt
+// once the workgroup's pair rows (columns [bx CB, (bx + 1) CB) of its tile's rows, whose pairs
+// are rowpair[0 .. rows)) are stored device-scope: one tile row (pair) per lane counts in for its token's column block in tok_cnt
 // [T, nbx] (zero on entry); the lanes whose count completes the token's k slots list their
 // tokens (s_tok, one int per lane), and the wave sums each listed token's k pair rows over the
 // block's columns: fp32 in slot order, + residual (bf16, when non-null) after one bf16 rounding,
 // one bf16 rounding into comb [T, N] (combine_kernel's arithmetic).
 template <int CB>
-__device__ __forceinline__ void handoff_combine(const int32_t* perm, int topk, int row0, int rows, int32_t* tok_cnt,
+__device__ __forceinline__ void handoff_combine(const int32_t* rowpair, int topk, int rows, int32_t* tok_cnt,
                                                 int nbx, int bx, const uint16_t* pairs, int N,
                                                 const uint16_t* residual, uint16_t* comb, int* s_tok) {
   const int lane = threadIdx.x & 63;
   bool done = false;
   int t = 0;
   if (lane < rows) {
-    t = perm[row0 + lane] / topk;
+    t = rowpair[lane] / topk;
     done = xwg_count_in(tok_cnt + (long)t * nbx + bx) == topk - 1;
   }
   const uint64_t mask = __ballot(done);

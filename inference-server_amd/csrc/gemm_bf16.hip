@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
       if (lane == 0) order = atomicAdd(&s_done, 1);
       order = __builtin_amdgcn_readfirstlane(order);
       if (order != CG - 1) return;
-      handoff_combine<CG * WCOLS>(p.perm, p.topk, row0, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N,
+      handoff_combine<CG * WCOLS>(p.perm + row0, p.topk, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N,
                                   nullptr, p.comb, s_tok);
       return;
     }

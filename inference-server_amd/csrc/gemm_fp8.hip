@@ -63,6 +63,9 @@ struct GemmArgs {
   int32_t* perm_out;  // [S]: identity (slot y holds pair y)
   int32_t* tiles_out; // [S, 4]: {expert, y, 1, 0}
   int32_t* n_tiles_out;
+  // expert buckets (decode tiles without a sort, moe_launch_route_buckets): the pairs of tile y's
+  // rows are bucket[tiles[y].w ...]
+  const int32_t* bucket;
 };
 
 constexpr int kMaxKB = 32;  // K <= 4096
@@ -89,6 +92,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   const int tile = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int e, row0, rows;
+  const int32_t* rowpair;  // the pairs of the tile's rows (gate_up's token rows, down's output rows)
   if constexpr (ROUTED) {
     // every wave routes the slot's token (the same bits in each: route_token is deterministic);
     // lane j < topk holds slot j's expert and weight
@@ -100,6 +104,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     e = __builtin_amdgcn_readlane(my_e, j);
     row0 = tile;
     rows = 1;
+    rowpair = p.perm_out + tile;
     if (writer && lane < p.topk) store_route(p.ids, p.id_bytes, p.wts, (long)t * p.topk + lane, my_e, my_w);
     if (blockIdx.x == 0 && wave == 0 && lane == 0) {
       *(int4*)(p.tiles_out + 4 * tile) = make_int4(e, tile, 1, 0);
@@ -112,6 +117,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     e = ti.x;
     row0 = ti.y;
     rows = ti.z;
+    rowpair = p.bucket != nullptr ? p.bucket + ti.w : p.perm + row0;
   }
 
   const int cg = wave % CG, ks = wave / CG;
@@ -153,7 +159,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 
   for (int r = threadIdx.x; r < BM; r += blockDim.x) {
     const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
-    s_arow[r] = ROUTED ? tile / p.topk : MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
+    s_arow[r] = ROUTED ? tile / p.topk : MODE == MODE_GATE_UP ? rowpair[min(r, rows - 1)] / p.topk : rr;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
@@ -294,7 +300,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
         v[0][q] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
         dst_row[q] = srow;
       } else {
-        const int pair = p.perm[srow];
+        const int pair = rowpair[min(r, rows - 1)];
         const float wt = bf16_to_f32(p.topk_w[pair]);
 #pragma unroll
         for (int o = 0; o < NOP; ++o) v[o][q] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
@@ -365,7 +371,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     }
   } else {
     static_assert(BM <= MOE_WAVE, "one tile row per lane");
-    handoff_combine<CG * WCOLS>(p.perm, p.topk, row0, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N, p.residual,
+    handoff_combine<CG * WCOLS>(rowpair, p.topk, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N, p.residual,
                                 p.comb, s_tok);
   }
 }
@@ -472,4 +478,31 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
   GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, wts, pairs, I, H, k, nullptr, nullptr, nullptr,
               tok_cnt, comb, residual};
   return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, S, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, S, s);
+}
+
+// The 16-row decode GEMMs on expert-bucket tiles (moe_launch_route_buckets: no sort launch): the
+// top-k kernel's last workgroup wrote the tile list, whose 4th field locates the tile's pairs in
+// the buckets; h rows are dense in expert order, as on the sorted path.  Same hand-offs as
+// moe_launch_grouped_gemms (tile_cnt for the h quantisation up to 2 pairs per expert, else a
+// quant_h launch; tok_cnt for the token combine), and the same bits.
+int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                                     const uint8_t* w2, const float* s2, const int32_t* bucket, const int32_t* tiles,
+                                     const int32_t* n_tiles, int T, int max_tiles, const uint16_t* topk_w,
+                                     uint16_t* h, uint8_t* hq, float* sh, uint16_t* pairs, int H, int I, int k,
+                                     hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
+                                     const uint16_t* residual) {
+  const int S = T * k;
+  GemmArgs g1{xq, sx, w13, s13, nullptr, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh, nullptr, nullptr,
+              nullptr};
+  g1.bucket = bucket;
+  int rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
+  if (rc) return rc;
+  if (tile_cnt == nullptr) {
+    rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
+    if (rc) return rc;
+  }
+  GemmArgs g2{hq, sh, w2, s2, nullptr, tiles, n_tiles, topk_w, pairs, I, H, k, nullptr, nullptr, nullptr,
+              tok_cnt, comb, residual};
+  g2.bucket = bucket;
+  return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
 }

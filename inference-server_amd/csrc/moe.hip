@@ -26,6 +26,16 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
                                     int32_t* perm, int32_t* tiles, int32_t* n_tiles, uint16_t* h, uint8_t* hq,
                                     float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s, int32_t* tile_cnt,
                                     int32_t* tok_cnt, uint16_t* comb, const uint16_t* residual);
+int moe_launch_route_buckets(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                             void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                             size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int32_t* zero, int nzero,
+                             int32_t* ecnt, int32_t* bucket, int32_t* tiles, int32_t* n_tiles);
+int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
+                                     const uint8_t* w2, const float* s2, const int32_t* bucket, const int32_t* tiles,
+                                     const int32_t* n_tiles, int T, int max_tiles, const uint16_t* topk_w,
+                                     uint16_t* h, uint8_t* hq, float* sh, uint16_t* pairs, int H, int I, int k,
+                                     hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
+                                     const uint16_t* residual);
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
                      void* logits, void* ids, int id_bytes, void* weights, void* workspace,
                      size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int block_m,
@@ -144,6 +154,9 @@ struct ExpertsWs {
   uint16_t* pairs;
   int32_t* cnt;    // 16-row tiles: the GEMMs' hand-off counters, [max_tiles, I/128] then [T, down column blocks]
   int n_cnt;       // 0 on the other paths
+  int32_t* ecnt;   // 16-row tiles: expert bucket counts [E] and a workgroup count, after the n_cnt counters
+  int n_ecnt;
+  int32_t* bucket; // 16-row tiles: expert buckets [E, T] of pair indices
   size_t total;
   int block_m;
   int max_tiles;
@@ -169,7 +182,10 @@ ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   w.sh = c.take<float>((size_t)S * (I / MOE_GROUP));
   w.pairs = c.take<uint16_t>((size_t)S * H);
   w.n_cnt = w.block_m != 16 ? 0 : w.max_tiles * (I / MOE_GROUP) + T * moe_down_col_blocks(S, H, w.block_m);
-  w.cnt = c.take<int32_t>(w.n_cnt);
+  w.n_ecnt = w.block_m != 16 ? 0 : E + 1;  // the bucket counts and the top-k's workgroup count
+  w.cnt = c.take<int32_t>(w.n_cnt + w.n_ecnt);  // one range, cleared by one launch
+  w.ecnt = w.cnt ? w.cnt + w.n_cnt : nullptr;
+  w.bucket = c.take<int32_t>(w.block_m != 16 ? 0 : (size_t)E * T);
   w.total = moe_align_up(c.off, 256);
   return w;
 }
@@ -324,6 +340,20 @@ int block_impl(const void* x, const void* w_router, int T, int H, int I, int E, 
                                            (uint16_t*)wt, w.perm, w.tiles, w.n_tiles, w.h, w.hq, w.sh, w.pairs, H, I,
                                            k, s, w.cnt, w.cnt + (long)w.max_tiles * (I / MOE_GROUP), (uint16_t*)out,
                                            (const uint16_t*)residual);
+  }
+  if (w.block_m == 16) {
+    // decode tiles: router GEMM (clearing the GEMMs' hand-off counters and the bucket counts), top-k
+    // into expert buckets, then the GEMMs on bucket tiles; no sort launch
+    int rc = moe_launch_route_buckets(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws, b.route_bytes,
+                                      s, w.xq, w.sx, w.cnt, w.n_cnt + w.n_ecnt, w.ecnt, w.bucket, w.tiles,
+                                      w.n_tiles);
+    if (rc) return rc;
+    const bool quant_handoff = T * k <= 2 * E;
+    return moe_launch_grouped_gemms_buckets(w.xq, w.sx, (const uint8_t*)w13, s13, (const uint8_t*)w2, s2, w.bucket,
+                                            w.tiles, w.n_tiles, T, w.max_tiles, (const uint16_t*)wt, w.h, w.hq, w.sh,
+                                            w.pairs, H, I, k, s, quant_handoff ? w.cnt : nullptr,
+                                            w.cnt + (long)w.max_tiles * (I / MOE_GROUP), (uint16_t*)out,
+                                            (const uint16_t*)residual);
   }
   // decode batches: x quantisation rides in the router GEMM, align in the top-k kernel; large
   // batches: the top-k kernel fills the expert sort's chunk histograms (cleared by the router

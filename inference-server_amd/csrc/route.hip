@@ -223,23 +223,57 @@ __global__ __launch_bounds__(256) void router_gemm_tiled_kernel(const uint16_t* 
 // One wave per token, 4 tokens per workgroup.  With `bc` (zeroed beforehand) each routed pair
 // also counts into its 1024-pair chunk's expert histogram bc[chunk][e], the first pass of the
 // expert sort (integer atomics: the counts do not depend on their order).
+//
+// With `ecnt` (the bucket counts [E] and, after them, one more int: a workgroup count, all zeroed
+// beforehand) each pair takes the next place of its expert's bucket instead, bucket[e * T + rank]
+// = pair, rank from an atomic count ecnt[e], and the last workgroup to count in writes the 16-row
+// decode tile list from the final counts: {expert, first dense row, rows, bucket offset}, experts
+// in order (the sorted path's tiles), and the tile count.  The order of the pairs inside a bucket
+// (the order of the atomics) changes no result: every tile row is computed on its own.
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restrict__ part, int ksplit,
                                                            const uint16_t* __restrict__ logits_in, int T,
                                                            int E, int k, int renorm,
                                                            uint16_t* __restrict__ logits_out, void* ids,
                                                            int id_bytes, uint16_t* __restrict__ weights,
-                                                           int32_t* __restrict__ bc) {
+                                                           int32_t* __restrict__ bc, int32_t* __restrict__ ecnt,
+                                                           int32_t* __restrict__ bucket, int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ n_tiles) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  int my_e;
-  float my_w;
-  route_token(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
-  if (bc != nullptr && lane < k) {
-    const int pair = t * k + lane;
-    atomicAdd(&bc[(long)(pair / kChunk) * (E + 1) + my_e], 1);
+  if (t < T) {
+    int my_e;
+    float my_w;
+    route_token(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
+    if (bc != nullptr && lane < k) {
+      const int pair = t * k + lane;
+      atomicAdd(&bc[(long)(pair / kChunk) * (E + 1) + my_e], 1);
+    }
+    // the atomic's returned rank is waited for, so the count is performed before the count-in below
+    if (ecnt != nullptr && lane < k) bucket[(long)my_e * T + atomicAdd(&ecnt[my_e], 1)] = t * k + lane;
+    if (lane < k) store_route(ids, id_bytes, weights, (long)t * k + lane, my_e, my_w);
   }
-  if (lane < k) store_route(ids, id_bytes, weights, (long)t * k + lane, my_e, my_w);
+  if (ecnt == nullptr) return;  // kernel-uniform
+  __shared__ int s_last;
+  __shared__ int s_cnt[kBuckets], s_off[kBuckets], s_toff[kBuckets];
+  xwg_wait_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = xwg_count_in(ecnt + E) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!s_last) return;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) s_cnt[e] = __hip_atomic_load(ecnt + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  scan_counts(s_cnt, E, 16, s_off, s_toff);
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    if (e == E) {
+      n_tiles[0] = s_toff[E];
+      continue;
+    }
+    const int c = s_cnt[e];
+    int tix = s_toff[e];
+    for (int r = 0; r < c; r += 16, ++tix)
+      *(int4*)(tiles + 4 * tix) = make_int4(e, s_off[e] + r, min(16, c - r), e * T + r);
+  }
 }
 
 // Decode batches (T * E <= kFusedMaxLogits, T * k <= 4096): routing and the stable
@@ -411,8 +445,24 @@ int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, i
   } else {
     MOE_LAUNCH(MOE_PROF_TOPK, s, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, part, ks_eff,
                (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights,
-               chunk_counts);
+               chunk_counts, (int32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr);
   }
+  MOE_CHECK_LAUNCH();
+  return MOE_OK;
+}
+
+// Router GEMM (clearing the nzero ints at `zero`, which must cover ecnt [E + 1]), then the top-k
+// with the expert buckets (bucket [E, T]) and the 16-row decode tile list (tiles, n_tiles).
+int moe_launch_route_buckets(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                             void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                             size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int32_t* zero, int nzero,
+                             int32_t* ecnt, int32_t* bucket, int32_t* tiles, int32_t* n_tiles) {
+  int ks_eff = 0;
+  int rc = moe_launch_router_gemm(x, w_router, T, H, E, workspace, workspace_bytes, s, xq, sx, zero, nzero, &ks_eff);
+  if (rc) return rc;
+  MOE_LAUNCH(MOE_PROF_TOPK, s, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0, s, (const float*)workspace,
+             ks_eff, (const uint16_t*)nullptr, T, E, k, renorm, (uint16_t*)logits, ids, id_bytes, (uint16_t*)weights,
+             (int32_t*)nullptr, ecnt, bucket, tiles, n_tiles);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -436,7 +486,8 @@ extern "C" int moe_mi355x_topk_softmax(const void* logits, int T, int E, int k, 
   MOE_RETURN_IF(!logits || !ids || !weights, MOE_ERR_INVALID_ARG);
   MOE_LAUNCH(MOE_PROF_TOPK, (hipStream_t)stream, topk_softmax_kernel, dim3((T + 3) / 4), dim3(256), 0,
              (hipStream_t)stream, (const float*)nullptr, 0, (const uint16_t*)logits, T, E, k, renorm,
-             (uint16_t*)nullptr, ids, id_bytes, (uint16_t*)weights, (int32_t*)nullptr);
+             (uint16_t*)nullptr, ids, id_bytes, (uint16_t*)weights, (int32_t*)nullptr, (int32_t*)nullptr,
+             (int32_t*)nullptr, (int32_t*)nullptr, (int32_t*)nullptr);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
