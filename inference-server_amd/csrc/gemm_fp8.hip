@@ -81,7 +81,12 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // rewritten as a uniform base + 32-bit lane offsets it fits 80 VGPRs (2 spilled) but still runs
 // slower at 6 waves (64 tokens 69.5 -> 86.3 us), and capped at 4 or 3 workgroups per CU (LDS
 // padding) slower as well (72.7 / 80.1 us): 5 is gate_up's best occupancy.
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
+// NKW > 0: every wave has exactly NKW K blocks (K = NKW * KS * 128), and the K loop is unrolled
+// with each block's loads issued one block ahead of its MFMAs and the wave's weight scales loaded
+// before the loop: in the rolled loop a scale load issued behind the next block's loads, and the
+// copy of the next block's registers into the current ones, wait for those loads inside the same
+// iteration, so a wave has only one block in flight.
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
@@ -156,6 +161,13 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
     for (int o = 0; o < NOP; ++o) bc[o] = *(const v8i*)(bptr[o] + ks * MOE_GROUP);
   }
+  float swk[NKW > 0 ? NKW : 1][NOP];  // NKW: the wave's weight scales, loaded up front
+  if constexpr (NKW > 0) {
+#pragma unroll
+    for (int i = 0; i < NKW; ++i)
+#pragma unroll
+      for (int o = 0; o < NOP; ++o) swk[i][o] = swp[o][ks + i * KS];
+  }
 
   for (int r = threadIdx.x; r < BM; r += blockDim.x) {
     const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
@@ -174,11 +186,9 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
     for (int o = 0; o < NOP; ++o) acc[mi][o] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  // the MFMAs of K block kb on activation fragments a and weight fragments bc
-  auto mfma_block = [&](const v8i (&a)[WM], int kb) __attribute__((always_inline)) {
-    float swv[NOP];
-#pragma unroll
-    for (int o = 0; o < NOP; ++o) swv[o] = swp[o][kb];
+  // the MFMAs of K block kb on activation fragments a and weight fragments b with weight scales swv
+  auto mfma_core = [&](const v8i (&a)[WM], const v8i (&b)[NOP], int kb, const float (&swv)[NOP])
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int mi = 0; mi < WM; ++mi) {
       float sav[4];
@@ -187,11 +197,18 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
       for (int o = 0; o < NOP; ++o) {
         const v4f zero = {0.f, 0.f, 0.f, 0.f};
-        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], bc[o], zero, 0, 0, 0, 0, 0, 0);
+        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], b[o], zero, 0, 0, 0, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[mi][o][q] = fmaf(t[q], sav[q] * swv[o], acc[mi][o][q]);
       }
     }
+  };
+  // the same on bc, with the weight scales loaded here
+  auto mfma_block = [&](const v8i (&a)[WM], int kb) __attribute__((always_inline)) {
+    float swv[NOP];
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) swv[o] = swp[o][kb];
+    mfma_core(a, bc, kb, swv);
   };
 
   if constexpr (SHA) {
@@ -228,6 +245,26 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
         for (int o = 0; o < NOP; ++o) bc[o] = bn[o];
       }
       __syncthreads();  // block kn visible, and every wave done with buffer kb & 1
+    }
+  } else if constexpr (NKW > 0) {
+    const uint8_t* aptr[WM];
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi) aptr[mi] = p.a + (long)s_arow[mi * 16 + lr] * p.K + lg * 32;
+    v8i av[NKW][WM], bv[NKW][NOP];
+#pragma unroll
+    for (int o = 0; o < NOP; ++o) bv[0][o] = bc[o];
+#pragma unroll
+    for (int mi = 0; mi < WM; ++mi) av[0][mi] = *(const v8i*)(aptr[mi] + ks * MOE_GROUP);
+#pragma unroll
+    for (int i = 0; i < NKW; ++i) {
+      if (i + 1 < NKW) {
+        const int kn = ks + (i + 1) * KS;
+#pragma unroll
+        for (int o = 0; o < NOP; ++o) bv[i + 1][o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
+#pragma unroll
+        for (int mi = 0; mi < WM; ++mi) av[i + 1][mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
+      }
+      mfma_core(av[i], bv[i], ks + i * KS, swk[i]);
     }
   } else {
     const uint8_t* aptr[WM];
@@ -376,18 +413,33 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
 }
 
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
-int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0>
+int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;
   // column blocks vary fastest: the workgroups past the live tiles (max_tiles is a bound)
   // come after every working one instead of between them, and consecutive workgroups stream
   // adjacent weight rows of one expert (gate_up at 64 tokens 75 -> 70 us)
   dim3 grid(a.N / (WCOLS * CG), max_tiles);
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED>),
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW>),
              grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
+}
+
+// The unrolled K loop where it pays: the 16-row down GEMM with 3 or 4 K blocks per wave (the
+// Qwen3-30B-A3B shape: 30B layer, down at 8 / 32 / 64 / 128 tokens 24.3 / 40.7 / 46.0 / 50.5 ->
+// 23.3 / 39.7 / 45.1 / 48.9 us).  Not for gate_up (its 4 blocks per wave took 94 VGPRs, one wave
+// per SIMD fewer: 1-2 us slower from 32 tokens) nor for 6 or 8 blocks (spills at the down GEMM's
+// 80-VGPR bound: Qwen3-235B-A22B down at 64 tokens 149 -> 169 us).
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
+int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
+  const int KB = a.K / MOE_GROUP;
+  if constexpr (MODE == MODE_DOWN && WM == 1 && !SHA) {
+    if (KB == 3 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 3>(a, max_tiles, s);
+    if (KB == 4 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 4>(a, max_tiles, s);
+  }
+  return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 0>(a, max_tiles, s);
 }
 
 }  // namespace

@@ -316,6 +316,8 @@ def test_block_fused_quant_is_bit_exact(pkg, dev, w30b, router30b, T):
 # with expert counts that are not powers of two, odd token counts and k = E.
 SHAPE_SWEEP = [
     (5, 256, 128, 8, 2),       # 16-row tiles, 10 pairs
+    (20, 512, 1024, 16, 4),    # 16-row tiles, 4 K blocks per down wave (the unrolled K loop)
+    (12, 256, 768, 32, 8),     # 16-row tiles, 3 K blocks per down wave, 8 pairs per token
     (9, 256, 128, 64, 32),     # the largest top-k
     (50, 256, 128, 256, 8),    # the largest expert count
     (1, 768, 256, 3, 3),       # k = E, one token
