@@ -429,8 +429,9 @@ int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
 
 // The unrolled K loop where it pays: the 16-row down GEMM with 3 or 4 K blocks per wave (the
 // Qwen3-30B-A3B shape: 30B layer, down at 8 / 32 / 64 / 128 tokens 24.3 / 40.7 / 46.0 / 50.5 ->
-// 23.3 / 39.7 / 45.1 / 48.9 us).  Not for gate_up (its 4 blocks per wave took 94 VGPRs, one wave
-// per SIMD fewer: 1-2 us slower from 32 tokens) nor for 6 or 8 blocks (spills at the down GEMM's
+// 23.3 / 39.7 / 45.1 / 48.9 us).  Not for gate_up: its 4 blocks per wave took 94 VGPRs and one
+// wave per SIMD fewer (1-2 us slower from 32 tokens), and held to 5 waves per SIMD (90 VGPRs) it
+// was slower still (64 tokens 69 -> 79 us); nor for 6 or 8 blocks (spills at the down GEMM's
 // 80-VGPR bound: Qwen3-235B-A22B down at 64 tokens 149 -> 169 us).
 template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
