@@ -248,14 +248,14 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
       const int pair = t * k + lane;
       atomicAdd(&bc[(long)(pair / kChunk) * (E + 1) + my_e], 1);
     }
-    // the atomic's returned rank is waited for, so the count is performed before the count-in below
     if (ecnt != nullptr && lane < k) bucket[(long)my_e * T + atomicAdd(&ecnt[my_e], 1)] = t * k + lane;
     if (lane < k) store_route(ids, id_bytes, weights, (long)t * k + lane, my_e, my_w);
   }
   if (ecnt == nullptr) return;  // kernel-uniform
   __shared__ int s_last;
   __shared__ int s_cnt[kBuckets], s_off[kBuckets], s_toff[kBuckets];
-  xwg_wait_stores();
+  // every wave's count atomics have returned (their ranks addressed the bucket stores): the
+  // workgroup's counts are performed; its other stores are read only by later launches
   __syncthreads();
   if (threadIdx.x == 0) s_last = xwg_count_in(ecnt + E) == (int)gridDim.x - 1;
   __syncthreads();
