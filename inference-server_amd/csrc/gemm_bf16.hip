@@ -41,6 +41,9 @@ struct Bf16GemmArgs {
   // (tok_cnt [T, column blocks], zero on entry; every id must be valid)
   int32_t* tok_cnt;
   uint16_t* comb;
+  // expert buckets (16-row tiles without a sort): the pairs of tile y's rows are
+  // bucket[tiles[y].w ...] (moe_launch_route_buckets)
+  const int32_t* bucket;
 };
 
 typedef uint4 Frag[4];  // the four 16-byte pieces of one lane for a 128-deep K block
@@ -56,6 +59,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
   if (tile >= p.n_tiles[0]) return;  // workgroup-uniform
   const int4 ti = *(const int4*)(p.tiles + 4 * tile);
   const int e = ti.x, row0 = ti.y, rows = ti.z;
+  const int32_t* rowpair = p.bucket != nullptr ? p.bucket + ti.w : p.perm + row0;  // the tile rows' pairs
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cg = wave % CG, ks = wave / CG;
@@ -90,7 +94,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
   }
   for (int r = threadIdx.x; r < BM; r += blockDim.x) {
     const int rr = row0 + min(r, rows - 1);  // rows past the tile end repeat the last row
-    s_arow[r] = MODE == MODE_GATE_UP ? p.perm[rr] / p.topk : rr;
+    s_arow[r] = MODE == MODE_GATE_UP ? rowpair[min(r, rows - 1)] / p.topk : rr;
   }
   __syncthreads();
   const uint16_t* aptr[WM];
@@ -176,7 +180,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
         int dst[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int pair = p.perm[row0 + min(mi * 16 + 4 * lg + q, rows - 1)];
+          const int pair = rowpair[min(mi * 16 + 4 * lg + q, rows - 1)];
           const float wt = bf16_to_f32(p.topk_w[pair]);
 #pragma unroll
           for (int o = 0; o < NOP; ++o) v[o][q] = f32_to_bf16(round_bf16(acc[mi][o][q]) * wt);
@@ -202,7 +206,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
       if (lane == 0) order = atomicAdd(&s_done, 1);
       order = __builtin_amdgcn_readfirstlane(order);
       if (order != CG - 1) return;
-      handoff_combine<CG * WCOLS>(p.perm + row0, p.topk, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N,
+      handoff_combine<CG * WCOLS>(rowpair, p.topk, rows, p.tok_cnt, gridDim.x, blockIdx.x, p.out, p.N,
                                   nullptr, p.comb, s_tok);
       return;
     }
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_bf16_kernel(Bf16GemmArgs p) 
       if constexpr (MODE == MODE_GATE_UP) {
         p.out[(long)srow * p.N + col] = f32_to_bf16(silu_mul_bf16(acc[mi][0][q], acc[mi][1][q]));
       } else {
-        const int pair = p.perm[srow];
+        const int pair = rowpair[r];
         const float wt = bf16_to_f32(p.topk_w[pair]);
 #pragma unroll
         for (int o = 0; o < NOP; ++o)
@@ -257,14 +261,15 @@ int moe_bf16_block_m(int S, int E, int H, int I) {
 }
 
 // gate_up (fused SiLU*up, bf16 h) then down (weighted pair rows; on 128-row tiles bf16(z) rows
-// that the combine weights), bf16 weights.
+// that the combine weights), bf16 weights.  With `bucket` (16-row tiles) the tile rows' pairs come
+// from the expert buckets instead of the sort's permutation.
 int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2, const int32_t* perm,
                                   const int32_t* tiles, const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w,
                                   uint16_t* h, uint16_t* pairs, int S, int H, int I, int k, int block_m,
-                                  hipStream_t s, int32_t* tok_cnt, uint16_t* comb) {
+                                  hipStream_t s, int32_t* tok_cnt, uint16_t* comb, const int32_t* bucket) {
   if (block_m == 128)
     return moe_launch_grouped_gemms_prefill_bf16(x, w13, w2, perm, tiles, n_tiles, max_tiles, h, pairs, H, I, k, s);
-  Bf16GemmArgs g1{x, w13, perm, tiles, n_tiles, nullptr, h, H, I, k, nullptr, nullptr};
+  Bf16GemmArgs g1{x, w13, perm, tiles, n_tiles, nullptr, h, H, I, k, nullptr, nullptr, bucket};
   int rc;
   if (block_m == 16)
     rc = launch_bf16_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
@@ -274,7 +279,8 @@ int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const 
     rc = launch_bf16_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
   // the token-combine hand-off on 16-row tiles (tok_cnt [T, H / 64]: CG 2 x 32 columns)
-  Bf16GemmArgs g2{h, w2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, block_m == 16 ? tok_cnt : nullptr, comb};
+  Bf16GemmArgs g2{h, w2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, block_m == 16 ? tok_cnt : nullptr, comb,
+                  bucket};
   if (block_m == 16)
     rc = launch_bf16_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s);
   else if (block_m == 32)

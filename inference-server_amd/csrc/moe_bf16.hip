@@ -11,7 +11,11 @@ int moe_bf16_block_m(int S, int E, int H, int I);
 int moe_launch_grouped_gemms_bf16(const uint16_t* x, const uint16_t* w13, const uint16_t* w2, const int32_t* perm,
                                   const int32_t* tiles, const int32_t* n_tiles, int max_tiles, const uint16_t* topk_w,
                                   uint16_t* h, uint16_t* pairs, int S, int H, int I, int k, int block_m,
-                                  hipStream_t s, int32_t* tok_cnt, uint16_t* comb);
+                                  hipStream_t s, int32_t* tok_cnt, uint16_t* comb, const int32_t* bucket);
+int moe_launch_route_buckets(const void* x, const void* w_router, int T, int H, int E, int k, int renorm,
+                             void* logits, void* ids, int id_bytes, void* weights, void* workspace,
+                             size_t workspace_bytes, hipStream_t s, uint8_t* xq, float* sx, int32_t* zero, int nzero,
+                             int32_t* ecnt, int32_t* bucket, int32_t* tiles, int32_t* n_tiles);
 int moe_launch_combine(const uint16_t* pairs, const void* ids, int id_bytes, const uint16_t* wts, int T, int k, int H,
                        int E, const uint16_t* residual, uint16_t* out, hipStream_t s);
 int moe_launch_route(const void* x, const void* w_router, int T, int H, int E, int k, int renorm, void* logits,
@@ -40,6 +44,8 @@ struct Bf16Ws {
   uint16_t* pairs;
   int32_t* cnt;  // 16-row tiles: the down GEMM's per-token hand-off counters [T, H / 64]
   int n_cnt;     // 0 on the other tiles
+  int32_t* ecnt;    // 16-row tiles: expert bucket counts [E] and a workgroup count, after cnt
+  int32_t* bucket;  // 16-row tiles: expert buckets [E, T] of pair indices
   size_t total;
   int block_m;
   int max_tiles;
@@ -61,7 +67,9 @@ Bf16Ws carve_bf16(void* base, int T, int H, int I, int E, int k) {
   w.h = c.take<uint16_t>((size_t)S * I);
   w.pairs = c.take<uint16_t>((size_t)S * H);
   w.n_cnt = w.block_m == 16 ? T * (H / 64) : 0;
-  w.cnt = c.take<int32_t>(w.n_cnt);
+  w.cnt = c.take<int32_t>(w.block_m == 16 ? w.n_cnt + E + 1 : 0);  // one range, cleared by the router
+  w.ecnt = w.cnt ? w.cnt + w.n_cnt : nullptr;
+  w.bucket = c.take<int32_t>(w.block_m == 16 ? (size_t)E * T : 0);
   w.total = moe_align_up(c.off, 256);
   return w;
 }
@@ -80,12 +88,12 @@ bool bf16_args_ok(int T, int H, int I, int E, int k, int id_bytes) {
 // 8 tokens 116.7 -> 114.3 us, 64 tokens 239.0 -> 235.8 us, Qwen3-30B-A3B shape).
 int bf16_experts_after_align(const void* x, const void* ids, int id_bytes, const void* weights, int T, int H, int I,
                              int E, int k, const void* w13, const void* w2, void* out, const Bf16Ws& w, hipStream_t s,
-                             bool ids_valid = false) {
+                             bool ids_valid = false, const int32_t* bucket = nullptr) {
   const bool fused_combine = ids_valid && w.n_cnt > 0 && T > 1;
   int rc = moe_launch_grouped_gemms_bf16((const uint16_t*)x, (const uint16_t*)w13, (const uint16_t*)w2, w.perm,
                                          w.tiles, w.n_tiles, w.max_tiles, (const uint16_t*)weights, w.h, w.pairs,
                                          T * k, H, I, k, w.block_m, s, fused_combine ? w.cnt : nullptr,
-                                         (uint16_t*)out);
+                                         (uint16_t*)out, bucket);
   if (rc) return rc;
   if (fused_combine) return MOE_OK;
   // the 128-row tiles leave the routing-weight product to the combine
@@ -163,6 +171,18 @@ extern "C" int moe_mi355x_block_bf16(const void* x, const void* w_router, int T,
   void* id_out = ids ? ids : (void*)b.ids;
   const int idb = ids ? id_bytes : 4;
   void* wt = weights ? weights : (void*)b.weights;
+  if (w.block_m == 16) {
+    // decode tiles: router GEMM (clearing the hand-off counters and the bucket counts), top-k into
+    // expert buckets with the tile list, then the GEMMs on bucket tiles; no sort launch (the FP8
+    // block's path; here, with GEMMs twice as long, level: 30B layer at 1 / 64 tokens 36.0 / 233.2 us
+    // either way)
+    int rc = moe_launch_route_buckets(x, w_router, T, H, E, k, renorm, lg, id_out, idb, wt, b.route_ws,
+                                      b.route_bytes, s, nullptr, nullptr, w.cnt, w.n_cnt + E + 1, w.ecnt, w.bucket,
+                                      w.tiles, w.n_tiles);
+    if (rc) return rc;
+    return bf16_experts_after_align(x, id_out, idb, wt, T, H, I, E, k, w13, w2, out, w, s, /*ids_valid=*/true,
+                                    w.bucket);
+  }
   // routing as the FP8 block, without the x quantisation; the sort rides in the top-k kernel
   // for decode batches, in its own launch(es) above
   const bool fused = moe_route_can_fuse_align(T, E, k);
