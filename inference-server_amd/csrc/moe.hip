@@ -315,9 +315,11 @@ namespace {
 // expert then stream its weights twice, which costs more than the launch saves from 5 tokens on
 // (Qwen3-30B-A3B layer: 1 / 2 / 4 tokens 31.7 / 38.1 / 50.8 -> 28.9 / 34.8 / 49.4 us; 5 / 8 tokens
 // 54.2 / 68.3 -> 56.1 / 75.6 us).
+// The slots are the tiles, so S = T k must fit the tile list and counters carved for at most
+// min(S, E) + S / 16 tiles: S <= E.
 constexpr int kRoutedMaxTokens = 4;
 bool routed_path(int T, int H, int E, int k, int block_m) {
-  return T <= kRoutedMaxTokens && block_m == 16 && T * k <= 2 * E && E <= 256 && !route_tiled_host(T, H);
+  return T <= kRoutedMaxTokens && block_m == 16 && T * k <= E && E <= 256 && !route_tiled_host(T, H);
 }
 
 // Router + experts; `residual` non-null adds it in the combine (moe_mi355x_moe_sublayer_fp8).

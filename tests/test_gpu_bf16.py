@@ -88,6 +88,10 @@ def test_bf16_block_matches_oracle(pkg, dev, T, H, I, E, k, bm):
     assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
     # the GEMMs accumulate exactly in fp32: nearly every output is the oracle's bf16 value
     assert (bf16_ulp_diff(got, ref) == 0).mean() >= 0.95
+    # the experts entry point (sorted tiles, separate combine) fed the block's routing gives the
+    # same bits as the block (expert-bucket tiles on 16-row tiles, combine inside the down GEMM)
+    again = pkg.experts_bf16(to_bf16(x, dev), ids, w, to_bf16(w13, dev), to_bf16(w2, dev))
+    assert torch.equal(out, again)
 
 
 def test_bf16_prefill_zipf_every_tile(pkg, dev):

@@ -321,6 +321,9 @@ SHAPE_SWEEP = [
     (9, 256, 128, 64, 32),     # the largest top-k
     (50, 256, 128, 256, 8),    # the largest expert count
     (1, 768, 256, 3, 3),       # k = E, one token
+    (2, 256, 128, 3, 3),       # 6 pairs on 3 experts: expert buckets (the routed path needs S <= E)
+    (2, 256, 128, 8, 3),       # routed one-row slots, two of them may name one expert
+    (4, 256, 128, 3, 3),       # 4 tokens on 3 experts: expert buckets
     (30, 512, 256, 10, 4),     # 32-row tiles
     (40, 384, 256, 6, 3),      # 64-row tiles (H % 256 != 0)
     (77, 1024, 384, 20, 5),    # 64-row tiles (I < 512)
