@@ -18,7 +18,9 @@ BLOCK = 128
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    # The raw handle of the current stream on t's device; the same value as
+    # torch.cuda.current_stream(t.device).cuda_stream without building a Stream object.
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def _need(t: torch.Tensor, name: str, dtypes, ndim: int | None = None) -> None:

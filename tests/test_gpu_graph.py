@@ -77,3 +77,13 @@ def test_graphed_block_buckets_match_eager(pkg, dev):
             assert got.shape == want.shape
             # padding rows change nothing in the real rows' routing or experts
             assert torch.equal(got, want), f"rep {rep} T={T}"
+
+
+def test_wrappers_launch_on_the_current_stream(pkg, dev):
+    from importlib import import_module
+    kernels = import_module(pkg.__name__ + ".kernels")
+    x = torch.zeros(4, device=dev)
+    assert kernels._stream(x) == torch.cuda.current_stream(dev).cuda_stream
+    side = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(side):
+        assert kernels._stream(x) == side.cuda_stream
