@@ -17,19 +17,20 @@ __device__ __forceinline__ uint32_t bf16_order_key(uint16_t b) {
   return (b & 0x8000u) ? (uint32_t)(~b & 0xffffu) : (uint32_t)(b | 0x8000u);
 }
 
-// Routing of one token by one wave.  Each lane holds experts lane, lane+64, lane+128,
-// lane+192.  Either sums the router's K-split partials (part != nullptr) and writes the
-// bf16 logits, or reads given logits.  Lane j < k returns the j-th expert (descending
+// Routing of one token by one wave.  Each lane holds experts lane, lane+64, ... (NC = E / 64
+// rounded up of them).  Either sums the router's K-split partials (part != nullptr) and writes
+// the bf16 logits, or reads given logits.  Lane j < k returns the j-th expert (descending
 // logit, ties to the lower id) and its (renormalised) weight before the bf16 cast.
-__device__ __forceinline__ void route_token(const float* __restrict__ part, int ksplit,
-                                            const uint16_t* __restrict__ logits_in, int T, int E, int k,
-                                            int renorm, uint16_t* __restrict__ logits_out, int t, int& my_e,
-                                            float& my_w) {
+template <int NC>
+__device__ __forceinline__ void route_token_nc(const float* __restrict__ part, int ksplit,
+                                               const uint16_t* __restrict__ logits_in, int T, int E, int k,
+                                               int renorm, uint16_t* __restrict__ logits_out, int t, int& my_e,
+                                               float& my_w) {
   const int lane = threadIdx.x & 63;
-  uint16_t lb[4];
-  bool valid[4];
+  uint16_t lb[NC];
+  bool valid[NC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int e = lane + 64 * c;
     valid[c] = e < E;
     lb[c] = 0;
@@ -54,20 +55,23 @@ __device__ __forceinline__ void route_token(const float* __restrict__ part, int 
   // softmax in fp32 (modeling_qwen3_moe.py:261)
   float m = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < NC; ++c)
     if (valid[c]) m = fmaxf(m, bf16_to_f32(lb[c]));
   m = wave_max_uniform(m);
-  float ex[4];
+  float ex[NC];
   float zsum = 0.f;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < NC; ++c) {
     ex[c] = valid[c] ? expf(bf16_to_f32(lb[c]) - m) : 0.f;
     zsum += ex[c];
   }
   zsum = wave_sum_uniform(zsum);
-  uint32_t key[4];
+  float prob[NC];  // the softmax, one division per expert (before the selection rounds)
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < NC; ++c) prob[c] = ex[c] / zsum;
+  uint32_t key[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
     key[c] = valid[c] ? ((bf16_order_key(lb[c]) << 16) | (0xffffu - (uint32_t)(lane + 64 * c))) : 0u;
   // top-k: k rounds of wave arg-max on (logit, -id)   (modeling_qwen3_moe.py:262)
   my_e = 0;
@@ -75,16 +79,16 @@ __device__ __forceinline__ void route_token(const float* __restrict__ part, int 
   for (int j = 0; j < k; ++j) {
     uint32_t best = key[0];
 #pragma unroll
-    for (int c = 1; c < 4; ++c) best = key[c] > best ? key[c] : best;
+    for (int c = 1; c < NC; ++c) best = key[c] > best ? key[c] : best;
     best = wave_max_u32_uniform(best);
     const int ew = (int)(0xffffu - (best & 0xffffu));
     const int owner = ew & 63, slot = ew >> 6;
     float pv = 0.f;
     if (lane == owner) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < NC; ++c)
         if (c == slot) {
-          pv = ex[c] / zsum;
+          pv = prob[c];
           key[c] = 0u;
         }
     }
@@ -96,6 +100,20 @@ __device__ __forceinline__ void route_token(const float* __restrict__ part, int 
     }
   }
   my_w = renorm ? my_p / psum : my_p;  // modeling_qwen3_moe.py:263-266
+}
+
+__device__ __forceinline__ void route_token(const float* __restrict__ part, int ksplit,
+                                            const uint16_t* __restrict__ logits_in, int T, int E, int k,
+                                            int renorm, uint16_t* __restrict__ logits_out, int t, int& my_e,
+                                            float& my_w) {
+  if (E <= 64)
+    route_token_nc<1>(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
+  else if (E <= 128)
+    route_token_nc<2>(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
+  else if (E <= 192)
+    route_token_nc<3>(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
+  else
+    route_token_nc<4>(part, ksplit, logits_in, T, E, k, renorm, logits_out, t, my_e, my_w);
 }
 
 __device__ __forceinline__ void store_route(void* ids, int id_bytes, uint16_t* weights, long idx, int e, float w) {

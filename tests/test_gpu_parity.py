@@ -324,6 +324,7 @@ SHAPE_SWEEP = [
     (2, 256, 128, 3, 3),       # 6 pairs on 3 experts: expert buckets (the routed path needs S <= E)
     (2, 256, 128, 8, 3),       # routed one-row slots, two of them may name one expert
     (4, 256, 128, 3, 3),       # 4 tokens on 3 experts: expert buckets
+    (2, 1536, 256, 16, 4),     # routed one-row slots, gate_up with 3 K blocks per wave unrolled
     (30, 512, 256, 10, 4),     # 32-row tiles
     (40, 384, 256, 6, 3),      # 64-row tiles (H % 256 != 0)
     (77, 1024, 384, 20, 5),    # 64-row tiles (I < 512)
