@@ -86,7 +86,10 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // before the loop: in the rolled loop a scale load issued behind the next block's loads, and the
 // copy of the next block's registers into the current ones, wait for those loads inside the same
 // iteration, so a wave has only one block in flight.
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0>
+// QH (16-row down GEMM): a holds bf16 h; the workgroup quantises its tile's rows into LDS (the
+// h quantisation's arithmetic: same codes and scales) and reads the activation fragments there.
+constexpr int kQhMaxK = 1024;  // 16 rows of LDS codes within the 6 workgroups per CU of the down GEMM
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0, bool QH = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
@@ -94,6 +97,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int BM = 16 * WM;
 
   static_assert(!ROUTED || (MODE == MODE_GATE_UP && WM == 1 && !SHA), "routed slots are one-row gate_up tiles");
+  static_assert(!QH || (MODE == MODE_DOWN && WM == 1 && !SHA), "h quantised in the 16-row down GEMM");
   const int tile = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int e, row0, rows;
@@ -147,6 +151,9 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   // conflict-free
   __shared__ __attribute__((aligned(16))) uint4 s_at[SHA ? 2 : 1][SHA ? BM * 8 : 1];
   static_assert(!SHA || (KS == 1 && BM * 8 == 256), "SHA stages one 16-byte chunk per thread, no K split");
+  // QH: the tile's e4m3 h rows; rows 16 B longer than K so that the 16 rows of a fragment read
+  // fall in distinct banks
+  __shared__ __attribute__((aligned(16))) uint8_t s_hq[QH ? BM : 1][QH ? kQhMaxK + 16 : 1];
   __shared__ int s_done;     // result waves past their hand-off stores
   __shared__ int s_tok[BM];  // down hand-off: tokens this workgroup combines
   if (threadIdx.x == 0) s_done = 0;  // visible after the barriers of the row setup below
@@ -181,11 +188,29 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     s_arow[r] = ROUTED ? tile / p.topk : MODE == MODE_GATE_UP ? rowpair[min(r, rows - 1)] / p.topk : rr;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
-    const int r = i / KB, kb = i % KB;
-    s_sa[r][kb] = p.sa[(long)s_arow[r] * KB + kb];
+  if constexpr (QH) {
+    // 16 lanes per (row, 128-column group), 8 values each; rows past the tile's end are not
+    // filled (their results are never stored)
+    const uint16_t* h = (const uint16_t*)p.a;
+    for (int i = threadIdx.x; i < rows * KB * 16; i += blockDim.x) {
+      const int r = i / (KB * 16), g = (i >> 4) - r * KB, sub = i & 15;
+      const uint4 raw = *(const uint4*)(h + (long)s_arow[r] * p.K + g * MOE_GROUP + sub * 8);
+      quant_group16_raw(raw, &s_hq[r][g * MOE_GROUP + sub * 8], &s_sa[r][g], sub);
+    }
+  } else {
+    for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
+      const int r = i / KB, kb = i % KB;
+      s_sa[r][kb] = p.sa[(long)s_arow[r] * KB + kb];
+    }
   }
   __syncthreads();
+  // the activation fragment of row lr (lane (lr, lg): bytes [32 lg, 32 lg + 32) of K block kb)
+  auto afrag = [&](const uint8_t* ptr, int kb) __attribute__((always_inline)) -> v8i {
+    if constexpr (QH)
+      return *(const v8i*)&s_hq[lr][kb * MOE_GROUP + lg * 32];
+    else
+      return *(const v8i*)(ptr + kb * MOE_GROUP);
+  };
 
   v4f acc[WM][NOP];
 #pragma unroll
@@ -261,7 +286,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
     for (int o = 0; o < NOP; ++o) bv[0][o] = bc[o];
 #pragma unroll
-    for (int mi = 0; mi < WM; ++mi) av[0][mi] = *(const v8i*)(aptr[mi] + ks * MOE_GROUP);
+    for (int mi = 0; mi < WM; ++mi) av[0][mi] = afrag(aptr[mi], ks);
 #pragma unroll
     for (int i = 0; i < NKW; ++i) {
       if (i + 1 < NKW) {
@@ -269,7 +294,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
         for (int o = 0; o < NOP; ++o) bv[i + 1][o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
 #pragma unroll
-        for (int mi = 0; mi < WM; ++mi) av[i + 1][mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
+        for (int mi = 0; mi < WM; ++mi) av[i + 1][mi] = afrag(aptr[mi], kn);
       }
       mfma_core(av[i], bv[i], ks + i * KS, swk[i]);
     }
@@ -281,7 +306,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     int kb = ks;
     if (kb < KB) {
 #pragma unroll
-      for (int mi = 0; mi < WM; ++mi) ac[mi] = *(const v8i*)(aptr[mi] + kb * MOE_GROUP);
+      for (int mi = 0; mi < WM; ++mi) ac[mi] = afrag(aptr[mi], kb);
     }
     for (; kb < KB; kb += KS) {
       v8i bn[NOP], an[WM];
@@ -290,7 +315,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
         for (int o = 0; o < NOP; ++o) bn[o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
 #pragma unroll
-        for (int mi = 0; mi < WM; ++mi) an[mi] = *(const v8i*)(aptr[mi] + kn * MOE_GROUP);
+        for (int mi = 0; mi < WM; ++mi) an[mi] = afrag(aptr[mi], kn);
       }
       mfma_block(ac, kb);
       if (kn < KB) {
@@ -420,7 +445,7 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
 }
 
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0>
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0, bool QH = false>
 int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
   constexpr int CG = 4 / KS;
   constexpr int WCOLS = MODE == MODE_GATE_UP ? 16 : 16 * DN;
@@ -428,7 +453,7 @@ int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
   // come after every working one instead of between them, and consecutive workgroups stream
   // adjacent weight rows of one expert (gate_up at 64 tokens 75 -> 70 us)
   dim3 grid(a.N / (WCOLS * CG), max_tiles);
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW>),
+  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW, QH>),
              grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
@@ -440,14 +465,30 @@ int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
 // wave per SIMD fewer (1-2 us slower from 32 tokens), and held to 5 waves per SIMD (90 VGPRs) it
 // was slower still (64 tokens 69 -> 79 us); nor for 6 or 8 blocks (spills at the down GEMM's
 // 80-VGPR bound: Qwen3-235B-A22B down at 64 tokens 149 -> 169 us).
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false>
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, bool QH = false>
 int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   const int KB = a.K / MOE_GROUP;
   if constexpr (MODE == MODE_DOWN && WM == 1 && !SHA) {
-    if (KB == 3 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 3>(a, max_tiles, s);
-    if (KB == 4 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 4>(a, max_tiles, s);
+    if (KB == 3 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 3, QH>(a, max_tiles, s);
+    if (KB == 4 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 4, QH>(a, max_tiles, s);
   }
-  return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 0>(a, max_tiles, s);
+  return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 0, QH>(a, max_tiles, s);
+}
+
+// The 16-row down GEMM quantises h itself (QH) where its tile's codes fit the LDS rows and the
+// unrolled loop stays within the 80-VGPR bound (4 K blocks per wave with two column slices
+// spills): no quant_h launch and no hand-off quantisation in gate_up, whose tail it lengthened.
+// Qwen3-30B-A3B layer at 8 / 16 / 32 / 64 tokens: 65.1 / 88.2 / 112.9 / 124.7 ->
+// 62.5 / 85.3 / 109.0 / 123.2 us (gate_up 36.1 / 50.8 / 66.0 -> 33.6 / 47.5 / 61.4 us; down level).
+bool down_quantises_h(int S, int I) { return I <= kQhMaxK && !(I / MOE_GROUP == 8 && S > 16); }
+
+// 16-row down GEMM: two column slices per wave beyond 2 tokens' pairs (T=8: down 25.7 -> 24.9 us;
+// level at 1, 32 and 64 tokens); g2.a / g2.sa are bf16 h / null with qh, else hq / its scales.
+int launch_down16(const GemmArgs& g2, int S, int max_tiles, bool qh, hipStream_t s) {
+  if (qh)
+    return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2, false, false, true>(g2, max_tiles, s)
+                  : launch_gemm<MODE_DOWN, 1, 2, 1, false, false, true>(g2, max_tiles, s);
+  return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
 }
 
 }  // namespace
@@ -478,9 +519,9 @@ int moe_down_col_blocks(int S, int H, int block_m) {
   return H / 64;                                       // CG 4 x 16 columns
 }
 
-// Decode-tile GEMMs (block_m 16 / 32 / 64) or the prefill GEMMs (128).  Decode tiles: with
-// tile_cnt (max_tiles x I/128 counters, zero on entry) gate_up quantises h itself and no quant_h launch
-// follows; with tok_cnt (T x moe_down_col_blocks counters, zero on entry) the down GEMM also sums
+// Decode-tile GEMMs (block_m 16 / 32 / 64) or the prefill GEMMs (128).  Decode tiles: 16-row down
+// GEMMs quantise h themselves where down_quantises_h; otherwise with tile_cnt (max_tiles x I/128
+// counters, zero on entry) gate_up quantises h and no quant_h launch follows; with tok_cnt (T x moe_down_col_blocks counters, zero on entry) the down GEMM also sums
 // each token's pair rows into comb (+ residual), and no combine launch is needed.
 int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, const int32_t* perm, const int32_t* tiles,
@@ -491,7 +532,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   if (block_m == 128)
     return moe_launch_grouped_gemms_prefill(xq, sx, w13, s13, w2, s2, perm, tiles, n_tiles, max_tiles, topk_w, hq,
                                             sh, pairs, H, I, k, s);
-  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh,
+  const bool qh = block_m == 16 && down_quantises_h(S, I);
+  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
               nullptr, nullptr, nullptr};
   int rc;
   if (block_m == 16)
@@ -501,17 +543,15 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   else
     rc = launch_gemm<MODE_GATE_UP, 4, 1>(g1, max_tiles, s);
   if (rc) return rc;
-  if (tile_cnt == nullptr) {
-    // one pass quantises h; quantising it inside the down GEMM instead would repeat the
-    // work in every one of the H/16 column waves that read a row
+  if (tile_cnt == nullptr && !qh) {
+    // one pass quantises h for the larger tiles, whose down GEMMs would each repeat it
     rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
     if (rc) return rc;
   }
-  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k, nullptr, nullptr, nullptr,
-              tok_cnt, comb, residual};
-  if (block_m == 16)  // beyond 2 tokens two column slices per wave stream more bytes per setup
-    // (T=8: down 25.7 -> 24.9 us; level at 1, 32 and 64 tokens)
-    rc = S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k,
+              nullptr, nullptr, nullptr, tok_cnt, comb, residual};
+  if (block_m == 16)
+    rc = launch_down16(g2, S, max_tiles, qh, s);
   else if (block_m == 32)
     rc = launch_gemm<MODE_DOWN, 2, 1, 2, true>(g2, max_tiles, s);
   else
@@ -522,7 +562,8 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
 // Single-token decode (one row per routing slot, S = T * k <= 2 E): gate_up routes its own slot
 // from the router GEMM's K-split partials (no top-k or sort launch) and writes the routing
 // outputs, the identity slot order and the one-row tile list; then the down GEMM of the 16-row
-// tiles with the in-launch h quantisation and token combine (tile_cnt and tok_cnt zero on entry).
+// tiles, which quantises h itself (else gate_up does, through tile_cnt), with the in-launch token
+// combine (tile_cnt and tok_cnt zero on entry).
 // Every expert GEMM row is computed as on the sorted path, so the bits are the same.
 int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                                     const uint8_t* w2, const float* s2, const float* part, int ksplit, int T, int E,
@@ -531,8 +572,9 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
                                     float* sh, uint16_t* pairs, int H, int I, int k, hipStream_t s, int32_t* tile_cnt,
                                     int32_t* tok_cnt, uint16_t* comb, const uint16_t* residual) {
   const int S = T * k;
-  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh, nullptr, nullptr,
-              nullptr, part, ksplit, T, E, renorm, logits, ids, id_bytes, wts, perm, tiles, n_tiles};
+  const bool qh = down_quantises_h(S, I);
+  GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
+              nullptr, nullptr, nullptr, part, ksplit, T, E, renorm, logits, ids, id_bytes, wts, perm, tiles, n_tiles};
   // gate_up with the wave's 3 or 4 K blocks unrolled (Qwen3-30B-A3B layer, 1 / 2 / 4 tokens:
   // gate_up 17.5 / 20.5 / 32.7 -> 16.2 / 20.1 / 31.0 us)
   const int KB1 = H / MOE_GROUP;
@@ -540,16 +582,21 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
            : KB1 == 12 ? launch_gemm_nkw<MODE_GATE_UP, 1, 4, 1, false, true, 3>(g1, S, s)
                        : launch_gemm<MODE_GATE_UP, 1, 4, 1, false, true>(g1, S, s);
   if (rc) return rc;
-  GemmArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, wts, pairs, I, H, k, nullptr, nullptr, nullptr,
-              tok_cnt, comb, residual};
-  return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, S, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, S, s);
+  GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, perm, tiles, n_tiles, wts, pairs, I, H, k,
+              nullptr, nullptr, nullptr, tok_cnt, comb, residual};
+  if (!qh && tile_cnt == nullptr) {
+    rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
+    if (rc) return rc;
+  }
+  return launch_down16(g2, S, S, qh, s);
 }
 
 // The 16-row decode GEMMs on expert-bucket tiles (moe_launch_route_buckets: no sort launch): the
 // top-k kernel's last workgroup wrote the tile list, whose 4th field locates the tile's pairs in
 // the buckets; h rows are dense in expert order, as on the sorted path.  Same hand-offs as
-// moe_launch_grouped_gemms (tile_cnt for the h quantisation up to 2 pairs per expert, else a
-// quant_h launch; tok_cnt for the token combine), and the same bits.
+// moe_launch_grouped_gemms (h quantised by the down GEMM where down_quantises_h, else through
+// tile_cnt up to 2 pairs per expert or a quant_h launch; tok_cnt for the token combine), and the
+// same bits.
 int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const uint8_t* w13, const float* s13,
                                      const uint8_t* w2, const float* s2, const int32_t* bucket, const int32_t* tiles,
                                      const int32_t* n_tiles, int T, int max_tiles, const uint16_t* topk_w,
@@ -557,17 +604,18 @@ int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const u
                                      hipStream_t s, int32_t* tile_cnt, int32_t* tok_cnt, uint16_t* comb,
                                      const uint16_t* residual) {
   const int S = T * k;
-  GemmArgs g1{xq, sx, w13, s13, nullptr, tiles, n_tiles, nullptr, h, H, I, k, tile_cnt, hq, sh, nullptr, nullptr,
-              nullptr};
+  const bool qh = down_quantises_h(S, I);
+  GemmArgs g1{xq, sx, w13, s13, nullptr, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
+              nullptr, nullptr, nullptr};
   g1.bucket = bucket;
   int rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
   if (rc) return rc;
-  if (tile_cnt == nullptr) {
+  if (tile_cnt == nullptr && !qh) {
     rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
     if (rc) return rc;
   }
-  GemmArgs g2{hq, sh, w2, s2, nullptr, tiles, n_tiles, topk_w, pairs, I, H, k, nullptr, nullptr, nullptr,
-              tok_cnt, comb, residual};
+  GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, nullptr, tiles, n_tiles, topk_w, pairs, I, H, k,
+              nullptr, nullptr, nullptr, tok_cnt, comb, residual};
   g2.bucket = bucket;
-  return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
+  return launch_down16(g2, S, max_tiles, qh, s);
 }
