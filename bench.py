@@ -65,12 +65,14 @@ class Shape:
 
     def gate_up_bytes(self, n_active, T):
         """Algorithmic HBM bytes of one gate_up launch: the active experts' W13 + scales,
-        the fp8 activations and their scales read, the intermediate written (up to 2 pairs per
-        expert, S <= 2 E, the launch quantises it itself: e4m3 codes + scales, and its bf16 h
-        round trip between the launch's workgroups is counted too; otherwise bf16 h)."""
+        the fp8 activations and their scales read, the intermediate written: bf16 h, which the
+        16-row down GEMM quantises as it loads it where its LDS rows hold I (I <= 1024); else up
+        to 2 pairs per expert (S <= 2 E) the launch quantises it itself (e4m3 codes + scales, and
+        its bf16 h round trip between the launch's workgroups is counted too)."""
         S = T * K_TOP
         out = 2 * S * self.I
-        if S <= 2 * self.E:
+        down_quantises = S <= 8 * self.E and self.I <= 1024 and not (self.I == 1024 and S > 16)
+        if S <= 2 * self.E and not down_quantises:
             out += 2 * S * self.I + S * self.I + 4 * S * (self.I // 128)
         return n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128) + out
 
@@ -109,7 +111,7 @@ S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 #   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
 #                         --copy-probe                                 -> 291,674 / 25,447 KiB
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): 195241 * 1024 * 2 + 768 * 1024,
+    ("qwen3-30b-a3b", 64): 194993 * 1024 * 2 + 768 * 1024,
     ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
 }
 
