@@ -23,15 +23,20 @@ def test_bytes_per_expert_235b():
 
 def test_gate_up_bytes_and_flops():
     s = bench.S30B
-    # activations in (fp8 + scales) and the intermediate out, on top of the weights: up to 2 pairs
-    # per expert (S = 256 <= 2 E) the launch also quantises h, so its bf16 h is written and read
-    # back once and the e4m3 codes and scales are written
-    S = 32 * 8
-    assert s.gate_up_bytes(10, 32) == (10 * 3_146_496 + 32 * 2048 + 4 * 32 * 16 + 2 * S * 768 + 2 * S * 768
-                                       + S * 768 + 4 * S * 6)
-    for T in (64, 256):  # above: bf16 h out only (a separate launch quantises it)
+    # activations in (fp8 + scales) and the intermediate out, on top of the weights: at the 30B
+    # shape (I = 768) the 16-row down GEMM quantises h, so gate_up writes bf16 h only
+    for T in (32, 64):
         S = T * 8
         assert s.gate_up_bytes(10, T) == 10 * 3_146_496 + T * 2048 + 4 * T * 16 + 2 * S * 768
+    # at the 235B shape (I = 1536 > 1024) gate_up quantises h itself up to 2 pairs per expert
+    # (S = 256 <= 2 E): its bf16 h is written and read back once and the e4m3 codes and scales are
+    # written; above, bf16 h only (a separate launch quantises it)
+    b = bench.S235B
+    S = 32 * 8
+    assert b.gate_up_bytes(10, 32) == (10 * b.gate_up_expert_bytes() + 32 * 4096 + 4 * 32 * 32 + 2 * S * 1536
+                                       + 2 * S * 1536 + S * 1536 + 4 * S * 12)
+    S = 64 * 8
+    assert b.gate_up_bytes(10, 64) == 10 * b.gate_up_expert_bytes() + 64 * 4096 + 4 * 64 * 32 + 2 * S * 1536
     assert s.gate_up_flops(4096) == 2 * 4096 * 8 * 1536 * 2048
     # the whole layer at a 4096-token chunk: 9,437,184 flop per pair + the router
     assert s.layer_flops(4096) == pytest.approx(4096 * 8 * 9_437_184 + 4096 * 2 * 2048 * 128)
