@@ -290,7 +290,7 @@ def bf16_sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
         beta, share = zipf
         router = zipf_router(torch, layer.wr, beta)
     xs = make_inputs(torch, dev, shape, T, 4, zipf_beta=beta)
-    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 3, router, xs)
+    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 20, router, xs)
     dur_ms = slots["gemm_gate_up"]
     entry = {"shape": shape.name, "experts_dtype": "bf16", "tokens": T, "us_per_layer": round(ms * 1e3, 2),
              "tokens_per_s": round(T / (ms * 1e-3), 1), "mean_active_experts": round(act, 2),
@@ -324,7 +324,7 @@ def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
         beta, share = zipf
         router = zipf_router(torch, layer.wr, beta)
     xs = make_inputs(torch, dev, shape, T, 4, zipf_beta=beta)
-    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 5, router, xs)
+    ms, slots, act, _ = run_config(pkg, torch, layer, T, steps, 20, router, xs)
     entry = {"shape": shape.name, "experts_dtype": "fp8", "tokens": T, "us_per_layer": round(ms * 1e3, 2),
              "tokens_per_s": round(T / (ms * 1e-3), 1),
              "us_per_layer_graph": round(graph_step_ms(pkg, torch, layer, T, steps, router, xs) * 1e3, 2),
@@ -526,8 +526,8 @@ def library_probe(torch, dev, reps=50):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -619,16 +619,16 @@ def main():
         sweep = []
         zipf = calibrate_zipf(pkg, torch, dev, layer)
         for Ts in (1, 8, 32, 64, 128, 256, 4096):
-            sweep.append(sweep_entry(pkg, torch, dev, layer, Ts, 20 if Ts < 4096 else 10,
+            sweep.append(sweep_entry(pkg, torch, dev, layer, Ts, 100 if Ts < 4096 else 20,
                                      zipf=zipf if Ts == 4096 else None))
         big = Layer(pkg, torch, dev, S235B, n_copies=2)
         for Ts in (64, 2048):
-            sweep.append(sweep_entry(pkg, torch, dev, big, Ts, 20 if Ts < 2048 else 10))
+            sweep.append(sweep_entry(pkg, torch, dev, big, Ts, 100 if Ts < 2048 else 20))
         del big
         torch.cuda.empty_cache()
         b16 = Bf16Layer(torch, dev, S30B, 2, layer.wr)
         for Ts in (1, 64, 4096):
-            sweep.append(bf16_sweep_entry(pkg, torch, dev, b16, Ts, 20 if Ts < 4096 else 10,
+            sweep.append(bf16_sweep_entry(pkg, torch, dev, b16, Ts, 100 if Ts < 4096 else 20,
                                           zipf=zipf if Ts == 4096 else None))
         del b16
         torch.cuda.empty_cache()
