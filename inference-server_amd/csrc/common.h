@@ -32,16 +32,83 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return (float)(__bf16)f; }
 
+// ---------------------------------------------------------------------------
+// Exact e4m3 dot products.  v_mfma_scale_f32_16x16x128_f8f6f4 aligns its 128 products to
+// the largest one and truncates the rest (about 2^-15 of the largest product is lost per
+// MFMA, always toward zero), so over a 4096-deep reduction the fp32 result drifts ~2^-14
+// of its value from the exact sum.  Widening the codes to bf16 (every e4m3 value is a bf16
+// value) and using v_mfma_f32_16x16x32_bf16, whose 8-bit x 8-bit products and their sum
+// are exact before the one fp32 rounding, gives the dequantise-then-fp32 result to fp32
+// rounding.  Each lane's 32-byte fragment (row l % 16, K bytes [32 (l / 16), +32)) feeds
+// four bf16 MFMAs, MFMA j taking bytes [8 j, 8 j + 8): the same K permutation for both
+// operands, and the same 16x16 result layout as the f8f6f4 MFMA.
+// ---------------------------------------------------------------------------
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 values, exactly (v_cvt_scalef32_pk_bf16_fp8, scale 1)
+__device__ __forceinline__ v8bf e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  const v2bf a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const v2bf b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const v2bf c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const v2bf d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return (v8bf){a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// The 16x16 block of sum_k a[k] b[k] over one 128-deep K block of e4m3 codes, exact up to fp32
+// rounding (a is the MFMA's A operand: rows of the result).  Both operands are widened just
+// before each MFMA: the code dwords pass through an empty volatile asm after the previous MFMA,
+// so the compiler cannot hoist the conversions of all four MFMAs ahead of the first (8 live
+// registers for the widened operands instead of 32; the kernels run at their register bounds).
+__device__ __forceinline__ v4f mfma_e4m3_exact(const v8i& a, const v8i& b) {
+  v4f t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t a0 = (uint32_t)a[2 * j], a1 = (uint32_t)a[2 * j + 1];
+    uint32_t b0 = (uint32_t)b[2 * j], b1 = (uint32_t)b[2 * j + 1];
+    asm volatile("" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
+    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3x8_to_bf16(a0, a1), e4m3x8_to_bf16(b0, b1), t, 0, 0, 0);
+    asm volatile("" : "+v"(t));
+  }
+  return t;
+}
+
+// Whether the expert GEMMs of a layer with hidden size H accumulate exactly.  With the
+// f8f6f4 MFMA's truncation the gate_up result of a 4096-deep reduction moves by ~2^-14 of its
+// value, enough to move bf16 h across an e4m3 rounding boundary of its re-quantisation for
+// ~0.2% of the intermediate codes; under a heavy routing weight one moved code shifts an
+// output of the Qwen3-235B-A22B layer (outputs up to ~2.9) by up to 3 bf16 ulps (2.3e-2).  At
+// H = 2048 (Qwen3-30B-A3B) the drift is half as large and outputs stay well within 2e-2, so the
+// f8f6f4 MFMA (twice the bf16 rate) is kept there.
+__host__ __device__ inline bool moe_exact_accum(int H) { return H > 2048; }
+
 // silu(gate) * up on bf16 values, in the reference's rounding order: the grouped GEMM
 // output is bf16, silu(gate) is rounded to bf16, the product is rounded again
-// (TF/integrations/moe.py:509-520).  sigmoid uses v_exp_f32 and v_rcp_f32 (about
-// 1 ulp); the bf16 roundings absorb that except at rare ties.
+// (TF/integrations/moe.py:509-520).  silu(g) = g / (1 + exp(-g)) with exp from v_exp_f32 (a few
+// ulps for the bf16 g of a layer) and the corrected quotient div_rn: silu(g) in fp32 is within a
+// few ulps of the reference's, and its bf16 rounding differs only where that value sits that close
+// to a bf16 rounding boundary.  The library expf was measured as well: ~30 more instructions per h
+// element (the 4096-token prefill gate_up 170 -> 198 us) for no measurable change in the e4m3
+// codes of h.
+__device__ __forceinline__ float div_rn(float a, float b);
 __device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
   const float g = round_bf16(gate_acc);
   const float u = round_bf16(up_acc);
   const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
-  const float sg = round_bf16(g * __builtin_amdgcn_rcpf(1.0f + e));
+  const float sg = round_bf16(div_rn(g, 1.0f + e));
   return round_bf16(sg * u);
+}
+
+// a / b for finite b != 0 away from the fp32 range limits (callers: |a| <= 2^64, b a group scale
+// or 1 + exp(-g) for a bf16 g): the v_rcp_f32 quotient with one residual correction.  The fma
+// residual a - q b is exact, so the corrected quotient is the correctly rounded one in all but
+// rare cases, and an exactly representable quotient (an e4m3 midpoint, say) always comes out
+// exact; the IEEE division sequence costs about three times as many instructions, which showed in
+// the prefill GEMM's epilogue (gate_up at 4096 tokens 170 -> 209 us).
+__device__ __forceinline__ float div_rn(float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q = a * r;
+  const float e = fmaf(-q, b, a);
+  return fmaf(e, r, q);
 }
 
 // ---------------------------------------------------------------------------

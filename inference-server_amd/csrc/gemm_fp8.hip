@@ -66,6 +66,8 @@ struct GemmArgs {
   // expert buckets (decode tiles without a sort, moe_launch_route_buckets): the pairs of tile y's
   // rows are bucket[tiles[y].w ...]
   const int32_t* bucket;
+  // exact accumulation (moe_exact_accum): e4m3 operands widened to bf16, bf16 MFMAs
+  int exact;
 };
 
 constexpr int kMaxKB = 32;  // K <= 4096
@@ -89,8 +91,9 @@ constexpr int kMaxKB = 32;  // K <= 4096
 // QH (16-row down GEMM): a holds bf16 h; the workgroup quantises its tile's rows into LDS (the
 // h quantisation's arithmetic: same codes and scales) and reads the activation fragments there.
 constexpr int kQhMaxK = 1024;  // 16 rows of LDS codes within the 6 workgroups per CU of the down GEMM
-template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0, bool QH = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? 6 : 1)))
+template <int MODE, int WM, int KS, int DN = 1, bool SHA = false, bool ROUTED = false, int NKW = 0, bool QH = false,
+          bool EX = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == MODE_DOWN && WM == 1 ? (EX ? 5 : 6) : 1)))
 void grouped_gemm_fp8_kernel(GemmArgs p) {
   constexpr int CG = 4 / KS;                  // column groups per workgroup
   constexpr int NOP = MODE == MODE_GATE_UP ? 2 : DN;  // B operands per wave (gate, up | column slices)
@@ -229,7 +232,11 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
 #pragma unroll
       for (int o = 0; o < NOP; ++o) {
         const v4f zero = {0.f, 0.f, 0.f, 0.f};
-        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], b[o], zero, 0, 0, 0, 0, 0, 0);
+        v4f t;
+        if constexpr (EX)
+          t = mfma_e4m3_exact(a[mi], b[o]);
+        else
+          t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[mi], b[o], zero, 0, 0, 0, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[mi][o][q] = fmaf(t[q], sav[q] * swv[o], acc[mi][o][q]);
       }
@@ -453,8 +460,12 @@ int launch_gemm_nkw(const GemmArgs& a, int max_tiles, hipStream_t s) {
   // come after every working one instead of between them, and consecutive workgroups stream
   // adjacent weight rows of one expert (gate_up at 64 tokens 75 -> 70 us)
   dim3 grid(a.N / (WCOLS * CG), max_tiles);
-  MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW, QH>),
-             grid, dim3(256), 0, s, a);
+  if (a.exact)
+    MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s,
+               (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW, QH, true>), grid, dim3(256), 0, s, a);
+  else
+    MOE_LAUNCH(MODE == MODE_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s,
+               (grouped_gemm_fp8_kernel<MODE, WM, KS, DN, SHA, ROUTED, NKW, QH, false>), grid, dim3(256), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -535,6 +546,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   const bool qh = block_m == 16 && down_quantises_h(S, I);
   GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
               nullptr, nullptr, nullptr};
+  g1.exact = moe_exact_accum(H);
   int rc;
   if (block_m == 16)
     rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
@@ -550,6 +562,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
   }
   GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, I, H, k,
               nullptr, nullptr, nullptr, tok_cnt, comb, residual};
+  g2.exact = moe_exact_accum(H);
   if (block_m == 16)
     rc = launch_down16(g2, S, max_tiles, qh, s);
   else if (block_m == 32)
@@ -575,6 +588,7 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
   const bool qh = down_quantises_h(S, I);
   GemmArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
               nullptr, nullptr, nullptr, part, ksplit, T, E, renorm, logits, ids, id_bytes, wts, perm, tiles, n_tiles};
+  g1.exact = moe_exact_accum(H);
   // gate_up with the wave's 3 or 4 K blocks unrolled (Qwen3-30B-A3B layer, 1 / 2 / 4 tokens:
   // gate_up 17.5 / 20.5 / 32.7 -> 16.2 / 20.1 / 31.0 us)
   const int KB1 = H / MOE_GROUP;
@@ -584,6 +598,7 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
   if (rc) return rc;
   GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, perm, tiles, n_tiles, wts, pairs, I, H, k,
               nullptr, nullptr, nullptr, tok_cnt, comb, residual};
+  g2.exact = moe_exact_accum(H);
   if (!qh && tile_cnt == nullptr) {
     rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
     if (rc) return rc;
@@ -607,6 +622,7 @@ int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const u
   const bool qh = down_quantises_h(S, I);
   GemmArgs g1{xq, sx, w13, s13, nullptr, tiles, n_tiles, nullptr, h, H, I, k, qh ? nullptr : tile_cnt, hq, sh,
               nullptr, nullptr, nullptr};
+  g1.exact = moe_exact_accum(H);
   g1.bucket = bucket;
   int rc = launch_gemm<MODE_GATE_UP, 1, 4>(g1, max_tiles, s);
   if (rc) return rc;
@@ -616,6 +632,7 @@ int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const u
   }
   GemmArgs g2{qh ? (const uint8_t*)h : hq, qh ? nullptr : sh, w2, s2, nullptr, tiles, n_tiles, topk_w, pairs, I, H, k,
               nullptr, nullptr, nullptr, tok_cnt, comb, residual};
+  g2.exact = moe_exact_accum(H);
   g2.bucket = bucket;
   return launch_down16(g2, S, max_tiles, qh, s);
 }

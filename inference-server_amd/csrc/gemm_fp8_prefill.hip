@@ -62,6 +62,7 @@ struct PrefillArgs {
   int N;                   // gate_up: I; down: H
   int topk;
   int n_nblk;              // column blocks per tile: gate_up I/128, down H/256
+  int exact;               // e4m3 operands widened to bf16 for exact bf16 MFMAs (moe_exact_accum)
 };
 
 // LDS rows are 128 bytes (eight 16-byte chunks).  Chunk c of row r is stored at position
@@ -152,8 +153,15 @@ __device__ __forceinline__ v8bf frag_half(const v8i& f, int h) {
 // bytes per row, so the LDS layout, the DMA and the fragment reads are the same; each fragment
 // feeds two v_mfma_f32_16x16x32_bf16 (lane group g supplies K chunks 2 g and 2 g + 1, the same
 // K permutation for both operands), which accumulate in fp32 in the MFMA: no scales, no FMAs.
-template <int MODE, bool BF>
+// EX: e4m3 operands, each 128-deep K block as four exact bf16 MFMAs on the widened codes (see
+// mfma_e4m3_exact) instead of one f8f6f4 MFMA.  A step slot takes one 32-deep quarter of one
+// weight fragment against the four activation fragments (four independent MFMAs; chaining a
+// tile's four quarters back to back stalled on each result), and the operands are widened just
+// before use, which keeps the kernel within its 256 VGPRs (widening whole fragments up front
+// spilled ~50 registers).
+template <int MODE, bool BF, bool EX = false>
 __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(PrefillArgs p) {
+  static_assert(!(BF && EX), "exact accumulation is for e4m3 operands");
   __shared__ __attribute__((aligned(16))) uint8_t s_ab[3][P_STAGE3];
   __shared__ __attribute__((aligned(16))) int s_perm[2][PBM];  // perm rows of the item, by item parity
   __shared__ __attribute__((aligned(16))) float s_swt[2][2][kMaxKB];  // its weight tile scales, per K block
@@ -313,11 +321,27 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       scb_[mi] = MODE == PF_GATE_UP ? SC[mi] * WC[1] : sca_[mi];                                  \
     }                                                                                             \
     v4f t_[4];                                                                                    \
+    v4f tx_[2][4];                                                                                \
     _Pragma("unroll") for (int it = 0; it < 21; ++it) {                                           \
-      if (it < 16) {                                                                              \
+      if (it < 16 && !EX) {                                                                       \
         const int ni = it >> 2, mi = it & 3;                                                      \
         t_[it & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(B[ni], AC[mi], zero4, 0, 0, 0, 0, 0, 0); \
         PF_PIN(t_[it & 3]);                                                                       \
+      }                                                                                           \
+      if (it < 16 && EX) {                                                                        \
+        /* slot (ni, jj): the jj-th 32-deep quarter of the K block for the four activation */      \
+        /* fragments, four independent exact MFMAs back to back */                                \
+        const int ni = it >> 2, jj = it & 3;                                                      \
+        uint32_t b0_ = (uint32_t)B[ni][2 * jj], b1_ = (uint32_t)B[ni][2 * jj + 1];                \
+        asm volatile("" : "+v"(b0_), "+v"(b1_));                                                  \
+        const v8bf bw_ = e4m3x8_to_bf16(b0_, b1_);                                                \
+        _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                        \
+          uint32_t a0_ = (uint32_t)AC[mi][2 * jj], a1_ = (uint32_t)AC[mi][2 * jj + 1];            \
+          asm volatile("" : "+v"(a0_), "+v"(a1_));                                                \
+          tx_[ni & 1][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                              \
+              bw_, e4m3x8_to_bf16(a0_, a1_), jj == 0 ? zero4 : tx_[ni & 1][mi], 0, 0, 0);         \
+          PF_PIN(tx_[ni & 1][mi]);                                                                \
+        }                                                                                         \
       }                                                                                           \
       switch (it) {                                                                               \
         case 0: PF_RD_A(AN, 0, 0); break;                                                         \
@@ -349,11 +373,21 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       if (it == 9) PF_DMA_ONE(4, ab_, bb_, sab_, sbw_);                                           \
       if (it == 11) PF_DMA_ONE(5, ab_, bb_, sab_, sbw_);                                          \
       if (it == 13) PF_DMA_ONE(6, ab_, bb_, sab_, sbw_);                                          \
-      if (it >= 3 && it < 19) {                                                                   \
+      if (!EX && it >= 3 && it < 19) {                                                            \
         const int j = it - 3, ni = j >> 2, mi = j & 3;                                            \
         const float sc_ = (MODE == PF_GATE_UP && ni >= 2) ? scb_[mi] : sca_[mi];                  \
         _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[mi][ni][q] = fmaf(t_[j & 3][q], sc_, acc[mi][ni][q]); \
         PF_PIN(acc[mi][ni]);                                                                      \
+      }                                                                                           \
+      if (EX && it >= 4 && it <= 16 && (it & 3) == 0) {                                           \
+        /* weight fragment ni's four results, one slot after its last quarter */                  \
+        const int ni = (it >> 2) - 1;                                                             \
+        _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                        \
+          const float sc_ = (MODE == PF_GATE_UP && ni >= 2) ? scb_[mi] : sca_[mi];                \
+          _Pragma("unroll") for (int q = 0; q < 4; ++q)                                           \
+            acc[mi][ni][q] = fmaf(tx_[ni & 1][mi][q], sc_, acc[mi][ni][q]);                       \
+          PF_PIN(acc[mi][ni]);                                                                    \
+        }                                                                                         \
       }                                                                                           \
       __builtin_amdgcn_sched_barrier(0);                                                          \
     }                                                                                             \
@@ -534,17 +568,15 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
         const float sc = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
         if (r < rows) {
           const long srow = row0 + r;
-          // h * (1/s) with a correctly rounded 1/s: within one fp32 ulp of h / s
-          const float inv_s = 1.0f / sc;
+          // h / s rounded as the oracle's division (div_rn): h and amax are bf16, so 448 h / amax
+          // often lands exactly on an e4m3 rounding midpoint, where h * (1 / s) (two roundings)
+          // falls on either side (0.05% of the codes differed that way)
           uint8_t* dst = p.hq + srow * p.N + nb * 128 + wn * 32 + 4 * lg;
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni) {
-            int code = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(acc[mi][ni][0] * inv_s),
-                                                       clamp_fp8(acc[mi][ni][1] * inv_s), 0, false);
-            code = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(acc[mi][ni][2] * inv_s),
-                                                   clamp_fp8(acc[mi][ni][3] * inv_s), code, true);
-            *(int*)(dst + ni * 16) = code;
-          }
+          for (int ni = 0; ni < 2; ++ni)
+            *(uint32_t*)(dst + ni * 16) = pack4_e4m3(clamp_fp8(div_rn(acc[mi][ni][0], sc)), clamp_fp8(div_rn(acc[mi][ni][1], sc)),
+                                                     clamp_fp8(div_rn(acc[mi][ni][2], sc)),
+                                                     clamp_fp8(div_rn(acc[mi][ni][3], sc)));
           if (wn == 0 && lg == 0) p.sh[srow * (p.N / PBK) + nb] = sc;
         }
       }
@@ -605,8 +637,12 @@ int launch_prefill(const PrefillArgs& a, int max_tiles, hipStream_t s) {
   if (g > max_items) g = max_items;
   g = (g + 7) / 8 * 8;
   if (g < 8) g = 8;
-  MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_prefill_kernel<MODE, BF>),
-             dim3((unsigned)g), dim3(P_THREADS), 0, s, a);
+  if (!BF && a.exact)
+    MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s,
+               (grouped_gemm_fp8_prefill_kernel<MODE, false, true>), dim3((unsigned)g), dim3(P_THREADS), 0, s, a);
+  else
+    MOE_LAUNCH(MODE == PF_GATE_UP ? MOE_PROF_GATE_UP : MOE_PROF_DOWN, s, (grouped_gemm_fp8_prefill_kernel<MODE, BF>),
+               dim3((unsigned)g), dim3(P_THREADS), 0, s, a);
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
@@ -624,10 +660,12 @@ int moe_launch_grouped_gemms_prefill(const uint8_t* xq, const float* sx, const u
   if (max_rows * (H > I ? H : I) >= (1L << 32)) return MOE_ERR_INVALID_ARG;
   // the cross-item DMA pipeline needs at least 4 K blocks per GEMM
   if (H / PBK < 4 || I / PBK < 4 || H % PBN != 0) return MOE_ERR_INVALID_ARG;
-  PrefillArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, nullptr, hq, sh, nullptr, H, I, k, I / PBK};
+  PrefillArgs g1{xq, sx, w13, s13, perm, tiles, n_tiles, nullptr, nullptr, hq, sh, nullptr, H, I, k, I / PBK,
+                 moe_exact_accum(H)};
   int rc = launch_prefill<PF_GATE_UP>(g1, max_tiles, s);
   if (rc) return rc;
-  PrefillArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, nullptr, nullptr, nullptr, I, H, k, H / PBN};
+  PrefillArgs g2{hq, sh, w2, s2, perm, tiles, n_tiles, topk_w, pairs, nullptr, nullptr, nullptr, I, H, k, H / PBN,
+                 moe_exact_accum(H)};
   return launch_prefill<PF_DOWN>(g2, max_tiles, s);
 }
 

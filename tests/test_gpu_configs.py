@@ -55,18 +55,14 @@ def tile_stratified_tokens(ids, E, block_m, rng):
     return np.array(sorted(toks)), len(tiles)
 
 
-def check_experts(pkg, dev, x, ids, w, weights_dev, weights_np, sub=None, scaled=False):
-    """``scaled``: the max-abs bar is 2e-2 times the largest reference magnitude (at least 1).  The
-    235B layer's outputs reach ~2.7, where one bf16 ulp is 1.6e-2, and the FP8 MFMA accumulates its
-    128 products with truncation (about 2^-20 of their absolute sum, measured on gfx950; the bf16 and
-    f16 MFMAs are exact to fp32): the resulting 1-3 ulp differences against the fp32 oracle exceed an
-    absolute 2e-2 at that magnitude while the mean error stays ~2e-3."""
+def check_experts(pkg, dev, x, ids, w, weights_dev, weights_np, sub=None):
+    """Layer output against the oracle at the absolute bar: max-abs <= 2e-2, mean-rel <= 1e-2."""
     out = pkg.experts_fp8(to_bf16(x, dev), to_dev(ids, dev), to_bf16(w, dev), *weights_dev)
     o = np_f32(out)
     sel = slice(None) if sub is None else sub
     ref = orc.experts_fp8(x[sel], ids[sel], w[sel], *weights_np, acc=np.float32)
     max_abs, mean_rel = errors(o[sel], ref)
-    bar = TOL_MAX_ABS * (max(1.0, float(np.abs(ref).max())) if scaled else 1.0)
+    bar = TOL_MAX_ABS
     print(f"max_abs {max_abs:.4g} (bar {bar:.4g}), mean_rel {mean_rel:.3g}, |ref| max {np.abs(ref).max():.3g}")
     assert max_abs <= bar and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
     return out
@@ -190,7 +186,7 @@ def test_c4_235b_decode_64_all_tokens(pkg, dev, w235b):
     x = orc.gen_normal_bf16(rng, (T, 4096))
     ids, w = orc.uniform_routing(rng, T, 128, 8)
     assert block_m_of(pkg, T, 4096, 1536, 128, 8) == 16
-    check_experts(pkg, dev, x, ids, w, *w235b, scaled=True)
+    check_experts(pkg, dev, x, ids, w, *w235b)
 
 
 @pytest.mark.timeout(600)
@@ -203,7 +199,7 @@ def test_c4_235b_prefill_2048_every_tile(pkg, dev, w235b):
     assert bm == 128
     sub, n_tiles = tile_stratified_tokens(ids, 128, bm, rng)
     assert n_tiles >= 128
-    check_experts(pkg, dev, x, ids, w, *w235b, sub=sub, scaled=True)
+    check_experts(pkg, dev, x, ids, w, *w235b, sub=sub)
 
 
 @pytest.mark.timeout(600)
@@ -220,5 +216,5 @@ def test_c4_235b_block_with_router(pkg, dev, w235b):
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     ref = orc.experts_fp8(x, ids_ref, w_ref, *wn, acc=np.float32)
     max_abs, mean_rel = errors(np_f32(out), ref)
-    assert max_abs <= TOL_MAX_ABS * max(1.0, float(np.abs(ref).max())) and mean_rel <= TOL_MEAN_REL, (max_abs,
-                                                                                                      mean_rel)
+    print(f"max_abs {max_abs:.4g}, mean_rel {mean_rel:.3g}, |ref| max {np.abs(ref).max():.3g}")
+    assert max_abs <= TOL_MAX_ABS and mean_rel <= TOL_MEAN_REL, (max_abs, mean_rel)
