@@ -68,8 +68,12 @@ class Shape:
         the fp8 activations and their scales read, the intermediate written: bf16 h, which the
         16-row down GEMM quantises as it loads it where its LDS rows hold I (I <= 1024); else up
         to 2 pairs per expert (S <= 2 E) the launch quantises it itself (e4m3 codes + scales, and
-        its bf16 h round trip between the launch's workgroups is counted too)."""
+        its bf16 h round trip between the launch's workgroups is counted too).  On the 128-row
+        prefill path the launch writes the e4m3 codes of h and their scales."""
         S = T * K_TOP
+        if self.prefill_path(T):  # the 128-row kernel writes the e4m3 codes of h and their scales
+            out = S * self.I + 4 * S * (self.I // 128)
+            return n_active * self.gate_up_expert_bytes() + T * self.H + 4 * T * (self.H // 128) + out
         out = 2 * S * self.I
         down_quantises = S <= 8 * self.E and self.I <= 1024 and not (self.I == 1024 and S > 16)
         if S <= 2 * self.E and not down_quantises:
@@ -111,8 +115,10 @@ S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 #   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
 #                         --copy-probe                                 -> 291,674 / 25,447 KiB
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): 194993 * 1024 * 2 + 768 * 1024,
-    ("qwen3-30b-a3b", 4096): 291674 * 1024 * 2 + 25447 * 1024,
+    ("qwen3-30b-a3b", 64): {"bytes": 194993 * 1024 * 2 + 768 * 1024,
+                            "source": "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc, build of 921578d)"},
+    ("qwen3-30b-a3b", 4096): {"bytes": 291674 * 1024 * 2 + 25447 * 1024,
+                              "source": "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc, build of 921578d)"},
 }
 
 
@@ -262,22 +268,34 @@ def graph_step_ms(pkg, torch, layer, T, steps, router, xs):
     return st.elapsed_time(en) / (reps * n_rot)
 
 
+RIDGE_FLOP_PER_BYTE = FP8_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # 625 flop/B
+
+
 def roofline_for(shape, T, slots, n_active):
-    """Roofline of the dominant kernel, gate_up: HBM-bound on the decode path (bytes of the
-    measured active experts), MFMA-bound on the 128-row prefill path."""
+    """Roofline of the dominant kernel, gate_up.  The bound follows its arithmetic intensity
+    (algorithmic flops over algorithmic HBM bytes of the measured active experts) against the
+    ridge of the FP8 peak and HBM (625 flop/B): below it the launch is HBM-bound and `frac` is
+    the HBM fraction, above it MFMA-bound and `frac` the FP8 fraction.  Both fractions are
+    reported (`hbm_frac`, `mfma_frac`): the prefill chunks sit just below the ridge (4096 tokens
+    ~470 flop/B), where both roofs are close."""
     dur_ms = slots["gemm_gate_up"]
     traffic = MEASURED_GATE_UP_TRAFFIC.get((shape.name, T))
-    if shape.prefill_path(T):
-        flops = shape.gate_up_flops(T)
-        achieved = flops / dur_ms / 1e9  # TFLOP/s
-        return {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
-                "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                "traffic": traffic, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+    flops = shape.gate_up_flops(T)
     byts = shape.gate_up_bytes(n_active, T)
-    achieved = byts / (dur_ms * 1e-3) / 1e9  # GB/s
-    return {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
+    gbs = byts / (dur_ms * 1e-3) / 1e9
+    tflops = flops / dur_ms / 1e9
+    intensity = flops / byts
+    out = {"kernel": "gemm_gate_up", "intensity_flop_per_byte": round(intensity, 1),
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+           "traffic": traffic["bytes"] if traffic else None,
+           "traffic_source": traffic["source"] if traffic else None,
+           "algorithmic_bytes": int(byts), "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+    if intensity >= RIDGE_FLOP_PER_BYTE:
+        out.update(bound="mfma", achieved=round(tflops, 1), peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
+                   frac=out["mfma_frac"])
+    else:
+        out.update(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=out["hbm_frac"])
+    return out
 
 
 def bf16_sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
@@ -295,21 +313,22 @@ def bf16_sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
     entry = {"shape": shape.name, "experts_dtype": "bf16", "tokens": T, "us_per_layer": round(ms * 1e3, 2),
              "tokens_per_s": round(T / (ms * 1e-3), 1), "mean_active_experts": round(act, 2),
              "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()}}
-    if shape.prefill_path(T):
-        flops = shape.gate_up_flops(T)
-        achieved = flops / dur_ms / 1e9
-        entry["roofline"] = {"bound": "mfma", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
-                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                             "traffic": None, "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
-        entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
-        entry["layer_bf16_peak_frac"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)
+    # bound by arithmetic intensity against the bf16 ridge (2.5 PFLOP/s over 8 TB/s = 312.5 flop/B)
+    flops = shape.gate_up_flops(T)
+    byts = shape.bf16_gate_up_bytes(act, T)
+    gbs = byts / (dur_ms * 1e-3) / 1e9
+    tflops = flops / dur_ms / 1e9
+    rf = {"kernel": "gemm_gate_up", "intensity_flop_per_byte": round(flops / byts, 1),
+          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+          "traffic": None, "algorithmic_bytes": int(byts), "algorithmic_flop": flops, "avg_us": round(dur_ms * 1e3, 2)}
+    if flops / byts >= BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9):
+        rf.update(bound="mfma", achieved=round(tflops, 1), peak=BF16_PEAK_TFLOPS, unit="TFLOP/s", frac=rf["mfma_frac"])
     else:
-        byts = shape.bf16_gate_up_bytes(act, T)
-        achieved = byts / (dur_ms * 1e-3) / 1e9
-        entry["roofline"] = {"bound": "hbm", "kernel": "gemm_gate_up", "achieved": round(achieved, 1),
-                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                             "traffic": None, "algorithmic_bytes": int(byts), "avg_us": round(dur_ms * 1e3, 2)}
-        entry["layer_hbm_frac"] = round(shape.bf16_layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        rf.update(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=rf["hbm_frac"])
+    entry["roofline"] = rf
+    entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
+    entry["layer_bf16_peak_frac"] = round(entry["layer_tflops"] / BF16_PEAK_TFLOPS, 4)
+    entry["layer_hbm_frac"] = round(shape.bf16_layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     if zipf is not None:
         entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
     print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
@@ -332,10 +351,10 @@ def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
              "kernels_us": {k: round(v * 1e3, 2) for k, v in slots.items()}}
     if zipf is not None:
         entry["routing"] = f"zipf s=1.1 bias, beta={beta:.3f}, top-10 share={share:.3f}"
-    if shape.prefill_path(T):
-        entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
-    else:
-        entry["layer_hbm_frac"] = round(shape.layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    entry["layer_tflops"] = round(shape.layer_flops(T) / (ms * 1e-3) / 1e12, 1)
+    entry["layer_mfma_frac"] = round(entry["layer_tflops"] / FP8_PEAK_TFLOPS, 4)
+    entry["layer_hbm_frac"] = round(shape.layer_bytes(act, T) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    entry["layer_bound"] = "mfma" if shape.layer_flops(T) / shape.layer_bytes(act, T) >= RIDGE_FLOP_PER_BYTE else "hbm"
     print(json.dumps({"sweep_progress": entry}), file=sys.stderr, flush=True)
     return entry
 

@@ -77,3 +77,33 @@ def test_bf16_bytes():
     assert s.bf16_gate_up_bytes(1, 1) == 2 * 2 * 768 * 2048 + 2 * 2048 + 2 * 8 * 768
     assert s.bf16_gate_up_bytes(126, 64) == 126 * 6_291_456 + 2 * 64 * 2048 + 2 * 512 * 768
     assert s.bf16_layer_bytes(126, 64) == 126 * 9_437_184 + 2 * 128 * 2048 + 4 * 64 * 2048
+
+
+def test_prefill_gate_up_bytes():
+    """On the 128-row path gate_up writes the e4m3 codes of h and one fp32 scale per 128 codes."""
+    s = bench.S30B
+    S = 4096 * 8
+    assert s.gate_up_bytes(128, 4096) == 128 * 3_146_496 + 4096 * 2048 + 4 * 4096 * 16 + S * 768 + 4 * S * 6
+
+
+@pytest.mark.parametrize("shape,T,bound", [(bench.S30B, 64, "hbm"), (bench.S30B, 256, "hbm"),
+                                           (bench.S30B, 4096, "hbm"), (bench.S235B, 64, "hbm"),
+                                           (bench.S235B, 2048, "hbm")])
+def test_roofline_bound_follows_intensity(shape, T, bound):
+    """The bound is chosen by the launch's flop per algorithmic byte against the 625 flop/B ridge
+    (5 PFLOP/s over 8 TB/s), not by the tile path: the 256-token batch (~32 flop/B) and even the
+    4096-token chunk (~470 flop/B, all 128 experts' weights streamed) sit below it."""
+    n_active = shape.expected_active(T)
+    r = bench.roofline_for(shape, T, {"gemm_gate_up": 0.1}, n_active)
+    intensity = shape.gate_up_flops(T) / shape.gate_up_bytes(n_active, T)
+    assert r["bound"] == bound and (intensity >= 625) == (bound == "mfma")
+    assert r["frac"] == (r["mfma_frac"] if bound == "mfma" else r["hbm_frac"])
+    # both fractions from the same duration
+    assert r["hbm_frac"] == pytest.approx(shape.gate_up_bytes(n_active, T) / 1e-4 / 8e12, abs=1e-4)
+    assert r["mfma_frac"] == pytest.approx(shape.gate_up_flops(T) / 1e-4 / 5e15, abs=1e-4)
+
+
+def test_mfma_bound_above_the_ridge():
+    """A hypothetical 64k-token chunk (~2000 flop/B) is MFMA-bound."""
+    r = bench.roofline_for(bench.S30B, 65536, {"gemm_gate_up": 1.0}, 128)
+    assert r["bound"] == "mfma" and r["unit"] == "TFLOP/s"
