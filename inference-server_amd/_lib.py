@@ -70,6 +70,10 @@ class MoEKernelError(RuntimeError):
     """A C-ABI entry point returned a non-zero code."""
 
 
+# (major << 16) | minor of the C ABI these signatures describe (moe_mi355x_version)
+ABI_VERSION = (0 << 16) | 2
+
+
 def load() -> ctypes.CDLL:
     """Load the shared library once; raises ImportError when it has not been built."""
     global _lib
@@ -87,6 +91,10 @@ def load() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            got = lib.moe_mi355x_version()
+            if got != ABI_VERSION:
+                raise ImportError(f"{LIB_PATH} has ABI version {got >> 16}.{got & 0xFFFF}, this binding expects "
+                                  f"{ABI_VERSION >> 16}.{ABI_VERSION & 0xFFFF}: rebuild it")
             _lib = lib
     return _lib
 

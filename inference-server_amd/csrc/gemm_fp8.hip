@@ -136,6 +136,9 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     e = ti.x;
     row0 = ti.y;
     rows = ti.z;
+    // Invariant: the tile list and the expert buckets come from an earlier launch (the top-k
+    // kernel's last workgroup writes them with plain stores and no release); only stream order
+    // makes them visible here, so they must never be read inside the launch that writes them.
     rowpair = p.bucket != nullptr ? p.bucket + ti.w : p.perm + row0;
   }
 

@@ -257,7 +257,8 @@ extern "C" const char* moe_mi355x_error_string(int code) {
   }
 }
 
-extern "C" int moe_mi355x_version(void) { return (0 << 16) | 1; }
+// 0.2: num_pages added to the paged-attention, KV-append and q/k-norm-rope-append entry points.
+extern "C" int moe_mi355x_version(void) { return (0 << 16) | 2; }
 
 extern "C" size_t moe_mi355x_experts_workspace_bytes(int T, int H, int I, int E, int k) {
   if (!experts_args_ok(T, H, I, E, k, 4)) return 0;

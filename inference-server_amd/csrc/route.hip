@@ -255,7 +255,10 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
   __shared__ int s_last;
   __shared__ int s_cnt[kBuckets], s_off[kBuckets], s_toff[kBuckets];
   // every wave's count atomics have returned (their ranks addressed the bucket stores): the
-  // workgroup's counts are performed; its other stores are read only by later launches
+  // workgroup's counts are performed; its other stores (bucket entries, ids, weights) carry no
+  // release, so they are read only by later launches (the decode GEMMs), which stream order
+  // orders after this one; a consumer inside this launch would need xwg_wait_stores() before the
+  // count-in below
   __syncthreads();
   if (threadIdx.x == 0) s_last = xwg_count_in(ecnt + E) == (int)gridDim.x - 1;
   __syncthreads();

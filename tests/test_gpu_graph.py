@@ -79,6 +79,57 @@ def test_graphed_block_buckets_match_eager(pkg, dev):
             assert torch.equal(got, want), f"rep {rep} T={T}"
 
 
+def _random_block(pkg, dev, E, H, I, k, seed, experts_dtype=torch.float8_e4m3fn):
+    block = pkg.MI355XSparseMoeBlock(E, H, I, k, device=dev, experts_dtype=experts_dtype)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    with torch.no_grad():
+        block.gate.weight.copy_((torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        if experts_dtype == torch.bfloat16:
+            block.experts.gate_up_proj.copy_((torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+            block.experts.down_proj.copy_((torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        else:
+            q13, s13, q2, s2 = gpu_weights(E, H, I, dev, seed=seed + 1)
+            block.experts.gate_up_proj.copy_(q13)
+            block.experts.gate_up_proj_scale_inv.copy_(s13)
+            block.experts.down_proj.copy_(q2)
+            block.experts.down_proj_scale_inv.copy_(s2)
+    return block
+
+
+def test_graphed_buckets_across_the_h_quantisation_switches(pkg, dev):
+    """I = 1536 > 1024: the h quantisation moves with the batch (routed one-row slots with the
+    gate_up hand-off up to 4 tokens here, expert buckets with the hand-off up to S = 2 E = 32
+    pairs, then a quant_h launch), and the buckets requested (2, 6, 12) straddle every switch:
+    padded replays equal eager bit for bit."""
+    E, H, I, k = 16, 256, 1536, 4
+    block = _random_block(pkg, dev, E, H, I, k, seed=21)
+    graphed = pkg.MI355XGraphedMoeBlock(block, buckets=(2, 6, 12))
+    rng = np.random.default_rng(12)
+    for rep in range(2):
+        for T in (1, 2, 3, 4, 5, 6, 7, 8, 9, 12):
+            x = to_bf16(orc.gen_normal_bf16(rng, (T, H)), dev).reshape(1, T, H)
+            want = block(x)
+            got = graphed(x)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"rep {rep} T={T}"
+
+
+def test_graphed_bf16_block_padded_bucket(pkg, dev):
+    """bf16 experts: bucket 2 fed one token (the one-token block combines in a separate launch,
+    larger ones inside the down GEMM): the padded replay equals eager bit for bit."""
+    E, H, I, k = 32, 512, 256, 8
+    block = _random_block(pkg, dev, E, H, I, k, seed=31, experts_dtype=torch.bfloat16)
+    graphed = pkg.MI355XGraphedMoeBlock(block, buckets=(2, 8))
+    rng = np.random.default_rng(13)
+    for rep in range(2):
+        for T in (1, 2, 5, 8):
+            x = to_bf16(orc.gen_normal_bf16(rng, (T, H)), dev).reshape(1, T, H)
+            want = block(x)
+            got = graphed(x)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"rep {rep} T={T}"
+
+
 def test_wrappers_launch_on_the_current_stream(pkg, dev):
     from importlib import import_module
     kernels = import_module(pkg.__name__ + ".kernels")
