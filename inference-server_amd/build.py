@@ -38,8 +38,8 @@ CFLAGS = [
 ]
 
 
-# Per-source extra flags.  The prefill GEMM keeps its MFMA results in VGPRs (its scale
-# FMAs read them there) instead of AGPRs, which would need a v_accvgpr_read per element.
+# Per-source extra flags.  The LDS-tiled prefill GEMM keeps its MFMA results in VGPRs (its
+# scale FMAs read them there) instead of AGPRs, which would need a v_accvgpr_read per element.
 EXTRA_FLAGS = {
     "gemm_fp8_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }

@@ -177,7 +177,7 @@ ExpertsWs carve_experts(void* base, int T, int H, int I, int E, int k) {
   w.n_tiles = c.take<int32_t>(4);
   w.align_ws_bytes = moe_mi355x_align_workspace_bytes(S, E);
   w.align_ws = c.take<char>(w.align_ws_bytes);
-  w.h = c.take<uint16_t>(w.block_m == 128 ? 0 : (size_t)S * I);  // the prefill GEMM quantises h in place
+  w.h = c.take<uint16_t>(w.block_m >= 128 ? 0 : (size_t)S * I);  // the prefill GEMM quantises h in place
   w.hq = c.take<uint8_t>((size_t)S * I);
   w.sh = c.take<float>((size_t)S * (I / MOE_GROUP));
   w.pairs = c.take<uint16_t>((size_t)S * H);
@@ -229,7 +229,7 @@ int launch_experts(const void* x, const void* ids, int id_bytes, const void* wei
                                 (const uint16_t*)residual);
   if (rc) return rc;
   if (fused_combine) return MOE_OK;
-  return moe_launch_combine(w.pairs, ids, id_bytes, w.block_m == 128 ? (const uint16_t*)weights : nullptr, T, k, H,
+  return moe_launch_combine(w.pairs, ids, id_bytes, w.block_m >= 128 ? (const uint16_t*)weights : nullptr, T, k, H,
                             E, (const uint16_t*)residual, (uint16_t*)out, s);
 }
 
