@@ -334,6 +334,8 @@ SHAPE_SWEEP = [
     (600, 512, 4096, 4, 2),    # the same on the 128-row prefill tiles
     (2, 256, 1536, 16, 4),     # routed one-row slots, h quantised in gate_up's hand-off (I > 1024)
     (6, 256, 1536, 32, 4),     # expert buckets, S <= 2 E: h quantised in gate_up's hand-off
+    (2, 256, 2048, 16, 4),     # the same two at I = 2048
+    (6, 256, 2048, 32, 4),
     (3, 256, 1024, 16, 4),     # the down GEMM quantises h itself with 4 K blocks per wave (NKW = 4)
     (5, 4096, 256, 8, 2),      # H > 2048: exact bf16 MFMAs on widened e4m3, 16-row tiles
     (30, 4096, 256, 10, 4),    # exact, 32-row tiles
