@@ -108,17 +108,15 @@ class Shape:
 S30B = Shape("qwen3-30b-a3b", 2048, 768)
 S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 
-# HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script
-# (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy):
-#   decode 64:            rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} ... -- python3 bench.py --no-sweep --no-cpu
-#                         --steps 10 --warmup 2 --copy-probe           -> 195,241 / 768 KiB
-#   prefill 4096, Zipf:   ... -- python3 bench.py --tokens 4096 --zipf --no-sweep --no-cpu --steps 5 --warmup 2
-#                         --copy-probe                                 -> 291,674 / 25,447 KiB
+# HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script on the build of
+# commit 224f085 (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy);
+# commands and per-dispatch figures in profiles/grouped_gemm_hbm_traffic.md:
+#   decode 64:            FETCH 195,265 / WRITE 768 KiB
+#   prefill 4096, Zipf:   FETCH 291,426 / WRITE 25,442 KiB
+_TRAFFIC_SRC = "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, build of 224f085)"
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): {"bytes": 194993 * 1024 * 2 + 768 * 1024,
-                            "source": "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc, build of 921578d)"},
-    ("qwen3-30b-a3b", 4096): {"bytes": 291674 * 1024 * 2 + 25447 * 1024,
-                              "source": "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc, build of 921578d)"},
+    ("qwen3-30b-a3b", 64): {"bytes": 195265 * 1024 * 2 + 768 * 1024, "source": _TRAFFIC_SRC},
+    ("qwen3-30b-a3b", 4096): {"bytes": 291426 * 1024 * 2 + 25442 * 1024, "source": _TRAFFIC_SRC},
 }
 
 
