@@ -165,4 +165,8 @@ def test_moe_sublayer_prologue_matches_oracle(pkg, dev, T):
     assert keep.sum() >= max(1, T // 2)
     d = np.abs(got[keep].astype(np.float64) - ref[keep])
     mean_rel = d.mean() / np.abs(blk[keep]).mean()  # relative to the block's contribution
-    assert d.max() <= 2e-2 * max(1.0, float(np.abs(ref).max()) / 4) and mean_rel <= 1e-2, (d.max(), mean_rel)
+    # the output is bf16(hs + block): a block within 2e-2 of the oracle's moves it by at most 2e-2
+    # plus one bf16 ulp of the output (the residual add's own rounding can fall the other way;
+    # hs ~ N(0, 2) reaches ~8, where one ulp is 6.3e-2)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref[keep]), 2.0 ** -126))) - 7)
+    assert np.all(d <= 2e-2 + ulp) and mean_rel <= 1e-2, (float((d - ulp).max()), mean_rel)
