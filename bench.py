@@ -45,7 +45,7 @@ FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
 LLC_BYTES = 256 * 2 ** 20
 K_TOP = 8
-N_SLOTS = 8  # kernel timing slots of the library (include/moe_mi355x.h)
+N_SLOTS = 9  # kernel timing slots of the library (include/moe_mi355x.h)
 
 
 @dataclass(frozen=True)

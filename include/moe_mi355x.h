@@ -226,6 +226,19 @@ int moe_mi355x_rms_norm(const void* x, const void* weight, int rows, int cols, f
                         void* stream);
 
 /*
+ * bf16 linear layer without bias: y = bf16(x @ w^T), fp32 accumulation, one rounding.  Replaces
+ * the nn.Linear projections of Qwen3MoeAttention.forward (q_proj / k_proj / v_proj fused into
+ * one weight, and o_proj), TF/models/qwen3_moe/modeling_qwen3_moe.py:162-164 and :189.
+ *   x bf16 [M, K]   w bf16 [N, K]   y bf16 [M, N]     N % 64 == 0, K % 128 == 0, 16-byte aligned
+ * The K dimension is split over workgroups when the output alone would not fill the GPU; the fp32
+ * partials then go to `workspace` (linear_bf16_workspace_bytes(M, N, K) bytes, 0 when no split)
+ * and are summed in a fixed order, so results do not depend on timing.
+ */
+size_t moe_mi355x_linear_bf16_workspace_bytes(int M, int N, int K);
+int moe_mi355x_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
  * The per-token tail of the q/k/v projections of a decode step: per-head RMSNorm of q and k
  * (q_norm / k_norm), the rotary embedding at positions[b] (cos / sin of positions[b] * inv_freq
  * in fp32, cast to bf16), q written out, k and v appended to the paged cache (layout of
@@ -265,7 +278,7 @@ int moe_mi355x_moe_sublayer_fp8(const void* h, const void* h_add, const void* ln
  * kernel launch of this library is bracketed by hipEvents on its stream; profile_read
  * waits for them and returns the launch count and summed duration (ms) of one slot:
  *   0 router_gemm  1 topk_softmax  2 quant_act  3 align  4 gemm_gate_up  5 quant_h
- *   6 gemm_down    7 combine
+ *   6 gemm_down    7 combine   8 linear
  * Enabling (or disabling) clears what was recorded.
  */
 int moe_mi355x_profile_enable(int on);

@@ -37,6 +37,7 @@ from .kernels import (  # noqa: F401
     moe_sublayer_fp8,
     paged_attention_decode,
     qk_norm_rope_append,
+    linear_bf16,
     rms_norm,
     quantize_act_fp8,
     quantize_weight_fp8,

@@ -52,6 +52,8 @@ SIGNATURES = {
     "moe_mi355x_kv_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                       _vp]),
     "moe_mi355x_rms_norm": (_c_int, [_vp, _vp, _c_int, _c_int, ctypes.c_float, _vp, _vp]),
+    "moe_mi355x_linear_bf16_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
+    "moe_mi355x_linear_bf16": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_size, _vp]),
     "moe_mi355x_qk_norm_rope_append": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                                 ctypes.c_float, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
     "moe_mi355x_moe_sublayer_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),

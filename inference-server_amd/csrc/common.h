@@ -368,7 +368,8 @@ enum {
   MOE_PROF_QUANT_H = 5,
   MOE_PROF_DOWN = 6,
   MOE_PROF_COMBINE = 7,
-  MOE_PROF_SLOTS = 8
+  MOE_PROF_LINEAR = 8,
+  MOE_PROF_SLOTS = 9
 };
 int moe_prof_begin(int slot, hipStream_t s);
 void moe_prof_end(int id, hipStream_t s);

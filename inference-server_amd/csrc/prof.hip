@@ -88,6 +88,6 @@ extern "C" int moe_mi355x_profile_read(int slot, int* count, double* total_ms) {
 
 extern "C" const char* moe_mi355x_profile_slot_name(int slot) {
   static const char* names[MOE_PROF_SLOTS] = {"router_gemm", "topk_softmax", "quant_act", "align",
-                                              "gemm_gate_up", "quant_h", "gemm_down", "combine"};
+                                              "gemm_gate_up", "quant_h", "gemm_down", "combine", "linear"};
   return (slot >= 0 && slot < MOE_PROF_SLOTS) ? names[slot] : "";
 }

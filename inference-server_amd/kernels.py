@@ -429,6 +429,28 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return out
 
 
+def linear_bf16(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``nn.Linear`` without bias on bf16 tensors: ``x [M, K] @ weight[N, K]^T`` with fp32
+    accumulation and one bf16 rounding (the q/k/v and o_proj projections of
+    ``Qwen3MoeAttention.forward``, TF/models/qwen3_moe/modeling_qwen3_moe.py:162-164, :189).
+    Needs N % 64 == 0 and K % 128 == 0."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(weight, "weight", torch.bfloat16, 2)
+    M, K = x.shape
+    N = weight.shape[0]
+    if weight.shape[1] != K:
+        raise ValueError(f"weight must be [N, {K}], got {tuple(weight.shape)}")
+    if N % 64 or K % 128:
+        raise ValueError("linear_bf16 needs N % 64 == 0 and K % 128 == 0")
+    lib = _lib.load()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    nws = lib.moe_mi355x_linear_bf16_workspace_bytes(M, N, K)
+    ws = _ws(nws, x.device)
+    _lib.check(lib.moe_mi355x_linear_bf16(x.data_ptr(), weight.data_ptr(), M, N, K, y.data_ptr(), ws.data_ptr(), nws,
+                                          _stream(x)), "moe_mi355x_linear_bf16")
+    return y
+
+
 def qk_norm_rope_append(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
                         inv_freq: torch.Tensor, positions: torch.Tensor, num_heads: int, num_kv_heads: int,
                         eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,

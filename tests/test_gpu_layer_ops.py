@@ -101,6 +101,33 @@ def test_qk_norm_rope_append_position_outside_the_table(pkg, dev):
     assert not kcn[[0, 1]].any() and not vcn[[0, 1]].any()  # sequence 0: nothing written
     assert kcn[2, :, 5, :].any() and vcn[2, :, :, 5].any()  # sequence 1: its slot
 
+@pytest.mark.parametrize("M,N,K", [(128, 5120, 2048), (128, 2048, 4096), (1, 1024, 256), (3, 256, 512),
+                                   (300, 64, 128), (129, 640, 1024), (1, 5120, 2048), (5, 1024, 4096),
+                                   (24, 2048, 4096), (40, 512, 2048), (64, 5120, 2048), (0, 64, 128)])
+def test_linear_bf16(pkg, dev, M, N, K):
+    """y = bf16(x @ w^T) against the exact product rounded once (fp64 sum of the exact bf16
+    products): the kernel accumulates in fp32 (the MFMA sums its products exactly, the K blocks are
+    added in fp32), so an output differs only where that fp32 sum sits within a few fp32 ulps of a
+    bf16 rounding boundary: at most 1 bf16 ulp (or 2^-20 of sum |x w| near zero), >= 99.9%
+    identical.  (128, 5120, 2048) and (128, 2048, 4096) are the decode step's q/k/v and o_proj at
+    batch 128; the shapes cover every row-tile count (1, 2, 4, 8 per wave), partial row blocks,
+    the K split (1 to 8 chunks and none) and an empty batch."""
+    rng = np.random.default_rng(M + N + K)
+    x = orc.round_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    w = orc.round_bf16((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    y = pkg.linear_bf16(to_bf16(x, dev), to_bf16(w, dev)).float().cpu().numpy()
+    if M == 0:
+        assert y.shape == (0, N)
+        return
+    ref = orc.round_bf16((x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32))
+    d = ulps(y, ref)
+    # near zero (cancellation) a few fp32 ulps of the summed magnitudes are many bf16 ulps of the
+    # result: there the bound is 2^-20 of sum |x w| (the fp32 accumulation's error)
+    mag = np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T
+    ok = (d <= 1) | (np.abs(y.astype(np.float64) - ref) <= 2.0 ** -20 * mag)
+    assert ok.all() and (d == 0).mean() >= 0.999, (int(d.max()), float((d == 0).mean()))
+
+
 @pytest.mark.parametrize("T", [1, 64, 600])
 def test_moe_sublayer_equals_separate_calls(pkg, dev, T):
     E, H, I, k = 32, 512, 256, 4
