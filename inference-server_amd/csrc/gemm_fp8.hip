@@ -103,6 +103,27 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   static_assert(!QH || (MODE == MODE_DOWN && WM == 1 && !SHA), "h quantised in the 16-row down GEMM");
   const int tile = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // ROUTED: the slot's token is known before its routing, and so are its activation scales and,
+  // with NKW, the wave's activation fragments: they are loaded here, so that their round trip
+  // overlaps the routing's (which reads what the router GEMM just wrote)
+  constexpr int kPreSa = ROUTED ? (16 * kMaxKB + 255) / 256 : 1;
+  float sa_pre[kPreSa];
+  v8i av_pre[ROUTED && NKW > 0 ? NKW : 1];
+  if constexpr (ROUTED) {
+    const int t = tile / p.topk;
+    const int KBr = p.K / MOE_GROUP;
+#pragma unroll
+    for (int u = 0; u < kPreSa; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      sa_pre[u] = i < BM * KBr ? p.sa[(long)t * KBr + i % KBr] : 0.f;
+    }
+    if constexpr (NKW > 0) {
+      const int ks_ = wave / (4 / KS);
+#pragma unroll
+      for (int i = 0; i < NKW; ++i)
+        av_pre[i] = *(const v8i*)(p.a + (long)t * p.K + (lane >> 4) * 32 + (ks_ + i * KS) * MOE_GROUP);
+    }
+  }
   int e, row0, rows;
   const int32_t* rowpair;  // the pairs of the tile's rows (gate_up's token rows, down's output rows)
   if constexpr (ROUTED) {
@@ -177,7 +198,10 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
   }
 
   v8i bc[NOP];
-  if (ks < KB) {
+  // with NKW every wave has K blocks (ks < KB): the loads are unconditional, since a branch
+  // around them makes the compiler wait for the first one where the branch joins, exposing its
+  // full memory latency before the row setup
+  if (NKW > 0 || ks < KB) {
 #pragma unroll
     for (int o = 0; o < NOP; ++o) bc[o] = *(const v8i*)(bptr[o] + ks * MOE_GROUP);
   }
@@ -202,6 +226,12 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
       const int r = i / (KB * 16), g = (i >> 4) - r * KB, sub = i & 15;
       const uint4 raw = *(const uint4*)(h + (long)s_arow[r] * p.K + g * MOE_GROUP + sub * 8);
       quant_group16_raw(raw, &s_hq[r][g * MOE_GROUP + sub * 8], &s_sa[r][g], sub);
+    }
+  } else if constexpr (ROUTED) {
+#pragma unroll
+    for (int u = 0; u < kPreSa; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < BM * KB) s_sa[i / KB][i % KB] = sa_pre[u];
     }
   } else {
     for (int i = threadIdx.x; i < BM * KB; i += blockDim.x) {
@@ -295,16 +325,23 @@ void grouped_gemm_fp8_kernel(GemmArgs p) {
     v8i av[NKW][WM], bv[NKW][NOP];
 #pragma unroll
     for (int o = 0; o < NOP; ++o) bv[0][o] = bc[o];
+    if constexpr (ROUTED) {
 #pragma unroll
-    for (int mi = 0; mi < WM; ++mi) av[0][mi] = afrag(aptr[mi], ks);
+      for (int i = 0; i < NKW; ++i) av[i][0] = av_pre[i];
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < WM; ++mi) av[0][mi] = afrag(aptr[mi], ks);
+    }
 #pragma unroll
     for (int i = 0; i < NKW; ++i) {
       if (i + 1 < NKW) {
         const int kn = ks + (i + 1) * KS;
 #pragma unroll
         for (int o = 0; o < NOP; ++o) bv[i + 1][o] = *(const v8i*)(bptr[o] + kn * MOE_GROUP);
+        if constexpr (!ROUTED) {
 #pragma unroll
-        for (int mi = 0; mi < WM; ++mi) av[i + 1][mi] = afrag(aptr[mi], kn);
+          for (int mi = 0; mi < WM; ++mi) av[i + 1][mi] = afrag(aptr[mi], kn);
+        }
       }
       mfma_core(av[i], bv[i], ks + i * KS, swk[i]);
     }

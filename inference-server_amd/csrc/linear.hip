@@ -221,6 +221,14 @@ int run_linear(const void* x, const void* w, int M, int N, int K, void* y, void*
   else if (c.nw == 4 && c.pf == 1)
     launch_linear_kernel<4, 1>(a, c.ks, s);
 #ifdef MOE_LINEAR_SWEEP
+  else if (c.nw == 5 && c.pf == 2)
+    launch_linear_kernel<5, 2>(a, c.ks, s);
+  else if (c.nw == 10 && c.pf == 2)
+    launch_linear_kernel<10, 2>(a, c.ks, s);
+  else if (c.nw == 5 && c.pf == 1)
+    launch_linear_kernel<5, 1>(a, c.ks, s);
+  else if (c.nw == 10 && c.pf == 1)
+    launch_linear_kernel<10, 1>(a, c.ks, s);
   else if (c.nw == 8 && c.pf == 2)
     launch_linear_kernel<8, 2>(a, c.ks, s);
   else if (c.nw == 8 && c.pf == 1)
