@@ -89,7 +89,8 @@ struct AttnArgs {
 // four waves per SIMD (at most 128 registers): each wave has one page in flight, so occupancy
 // is what keeps the HBM busy
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void paged_attn_decode_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps page ids and descriptors scalar
   const int lr = lane & 15, lg = lane >> 4;
   const int G = a.Hq / a.Hkv;
 
@@ -179,18 +180,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   // displacing what the caches hold for reuse (5.24 -> 5.40 TB/s at the config-5 batch), issued
   // as buffer loads on a per-(page, kv head) descriptor (SGPR base, 32-bit lane offsets within
   // the 4 KB block: 215.9 -> 212.4 us against global loads)
-  auto load_k = [&](int p) __attribute__((always_inline)) {
+  // live == false (no such page): a zero-size descriptor, so the loads read zeros and touch no
+  // memory.  Loads are issued unconditionally this way because a branch around them makes the
+  // compiler wait for them where the branch joins: the next page's loads behind an `if` had every
+  // iteration wait for them before its last output MFMA.
+  auto load_k = [&](int p, bool live) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const bool ok = page_ok(pg);
+    const bool ok = live && page_ok(pg);
     const __amdgpu_buffer_rsrc_t rk = kv_rsrc(a.k_cache + ((ok ? pg : 0) * a.Hkv + g) * kv_head_stride, ok);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       kr[kk] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, (lr * kHD + 32 * kk + 8 * lg) * 2, 0,
                                                                                  kCachePolicyNT));
   };
-  auto load_v = [&](int p) __attribute__((always_inline)) {
+  auto load_v = [&](int p, bool live) __attribute__((always_inline)) {
     const long pg = page_of(p);
-    const bool ok = page_ok(pg);
+    const bool ok = live && page_ok(pg);
     const __amdgpu_buffer_rsrc_t rv = kv_rsrc(a.v_cache + ((ok ? pg : 0) * a.Hkv + g) * kv_head_stride, ok);
 #pragma unroll
     for (int n = 0; n < 8; ++n)
@@ -199,10 +204,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   };
 
   int p = p_begin + wave;
-  if (p < p_end) {
-    load_k(p);
-    load_v(p);
-  }
+  load_k(p, p < p_end);
+  load_v(p, p < p_end);
   for (; p < p_end; p += kAttnWaves) {
     const bool more = p + kAttnWaves < p_end;
     // scores S^T: lane holds keys 4 lg + i of head lr
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
       s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kr[kk]), qop[kk], s, 0, 0, 0);
-    if (more) load_k(p + kAttnWaves);
+    load_k(p + kAttnWaves, more);
     const int key0 = p * kPage + 4 * lg;
     const int key_end = page_ok(page_of(p)) ? ctx : 0;  // an empty page has no live keys
     float sv[4];
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       va[3] = (short)(vy >> 16);
       o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[n], 0, 0, 0);
     }
-    if (more) load_v(p + kAttnWaves);
+    load_v(p + kAttnWaves, more);
   }
 
   // merge the 4 waves: per head max, sum and O rows (head lr, dims 16 n + 4 lg + i)
