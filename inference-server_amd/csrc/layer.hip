@@ -16,10 +16,13 @@ constexpr int kHD = 128;
 constexpr int kPage = 16;
 
 // y = bf16(w * bf16(x * r)), r = 1 / sqrt(sum(x^2) / C + eps): one wave per row, C <= 8192,
-// C % 8 == 0.  The row is read once into registers (16-byte loads).  With `add` non-null the
-// normalised row is x = bf16(x + add) (the decoder layer's residual add before the
-// post-attention norm, modeling_qwen3_moe.py:341), also written to `sum_out` when non-null.
-template <int MAXV>  // uint4 chunks (8 values) per lane
+// C % 8 == 0.  The row, its residual addend (ADD) and the norm weight are all loaded at the start
+// (16-byte loads), unconditionally: a lane past the row's end reloads the last chunk and zeroes
+// it (a branch around loads makes the compiler wait for them where it joins, and the weight,
+// loaded after the row's sum, cost a second round trip).  With ADD the normalised row is
+// x = bf16(x + add) (the decoder layer's residual add before the post-attention norm,
+// modeling_qwen3_moe.py:341), also written to `sum_out` when non-null.
+template <int MAXV, bool ADD>  // uint4 chunks (8 values) per lane
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ add,
                                                        const uint16_t* __restrict__ w, int R, int C, float eps,
                                                        uint16_t* __restrict__ out, uint16_t* __restrict__ sum_out) {
@@ -30,15 +33,20 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restric
   if (row >= R) return;
   const int lane = threadIdx.x & 63;
   const uint16_t* xr = x + (long)row * C;
-  uint4 v[MAXV];
+  uint4 v[MAXV], av[MAXV], wv[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = min((i * 64 + lane) * 8, C - 8);
+    v[i] = *(const uint4*)(xr + c);
+    if constexpr (ADD) av[i] = *(const uint4*)(add + (long)row * C + c);
+    wv[i] = *(const uint4*)(w + c);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     const int c = (i * 64 + lane) * 8;
-    v[i] = c < C ? *(const uint4*)(xr + c) : make_uint4(0, 0, 0, 0);
-    if (add != nullptr && c < C) {
-      const uint4 av = *(const uint4*)(add + (long)row * C + c);
-      const uint32_t xu[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, au[4] = {av.x, av.y, av.z, av.w};
+    if constexpr (ADD) {
+      const uint32_t xu[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, au[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
       uint32_t su[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -47,8 +55,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restric
         su[j] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
       }
       v[i] = make_uint4(su[0], su[1], su[2], su[3]);
-      if (sum_out != nullptr) *(uint4*)(sum_out + (long)row * C + c) = v[i];
+      if (sum_out != nullptr && c < C) *(uint4*)(sum_out + (long)row * C + c) = v[i];
     }
+    if (c >= C) v[i] = make_uint4(0, 0, 0, 0);  // past the row: contributes nothing, never stored
     const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -63,9 +72,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restric
   for (int i = 0; i < MAXV; ++i) {
     const int c = (i * 64 + lane) * 8;
     if (c >= C) continue;
-    const uint4 wv = *(const uint4*)(w + c);
     const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    const uint32_t wu[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t wu[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -98,7 +106,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   const int b = item / nh, h = item % nh;
   const int lane = threadIdx.x & 63;
   const uint16_t* src = qkv + ((long)b * nh + h) * kHD;
-  float x0 = bf16_to_f32(src[lane]), x1 = bf16_to_f32(src[lane + 64]);
+  // every load that depends only on the item goes out first (the norm weight and the rotary
+  // frequency too, used after the head's sum), so a q head costs one round trip
+  const uint16_t* nw = h < Hq ? qw : kw;
+  const uint16_t s0 = src[lane], s1 = src[lane + 64];
+  const uint16_t w0 = nw[lane], w1 = nw[lane + 64];
+  const float ifreq = inv_freq[lane];
+  float x0 = bf16_to_f32(s0), x1 = bf16_to_f32(s1);
   const int pos = positions[b];
   // a position outside the block table, or a table entry outside the pools (a -1 pad, a stale
   // id), has no page: q is still written, the cache is not
@@ -109,17 +123,16 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(
   if (h >= Hq + Hkv) {  // v head: transposed page rows
     const int g = h - Hq - Hkv;
     uint16_t* dst = v_cache + (page * Hkv + g) * (long)(kHD * kPage);
-    dst[lane * kPage + slot] = src[lane];
-    dst[(lane + 64) * kPage + slot] = src[lane + 64];
+    dst[lane * kPage + slot] = s0;
+    dst[(lane + 64) * kPage + slot] = s1;
     return;
   }
-  const uint16_t* nw = h < Hq ? qw : kw;
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float r = 1.0f / sqrtf(ss / (float)kHD + eps);
-  x0 = round_bf16(bf16_to_f32(nw[lane]) * round_bf16(x0 * r));
-  x1 = round_bf16(bf16_to_f32(nw[lane + 64]) * round_bf16(x1 * r));
+  x0 = round_bf16(bf16_to_f32(w0) * round_bf16(x0 * r));
+  x1 = round_bf16(bf16_to_f32(w1) * round_bf16(x1 * r));
   // cos / sin of pos * inv_freq[lane] (both halves of emb = cat(freqs, freqs) share it)
-  const float f = (float)pos * inv_freq[lane];
+  const float f = (float)pos * ifreq;
   const float c = round_bf16(cosf(f)), s = round_bf16(sinf(f));
   // element lane: x0 * cos - x1 * sin; element lane + 64: x1 * cos + x0 * sin (bf16 steps)
   const float y0 = round_bf16(round_bf16(x0 * c) + round_bf16(-x1 * s));
@@ -141,15 +154,22 @@ int moe_launch_rms_norm(const void* x, const void* add, const void* w, int R, in
   if (R <= 0) return MOE_OK;
   const dim3 grid((R + 3) / 4), block(256);
   const int chunks = (C / 8 + 63) / 64;
+#define MOE_RMS(V_)                                                                                        \
+  do {                                                                                                     \
+    if (add != nullptr)                                                                                    \
+      hipLaunchKernelGGL((rms_norm_kernel<V_, true>), grid, block, 0, s, (const uint16_t*)x,               \
+                         (const uint16_t*)add, (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out); \
+    else                                                                                                   \
+      hipLaunchKernelGGL((rms_norm_kernel<V_, false>), grid, block, 0, s, (const uint16_t*)x,              \
+                         (const uint16_t*)add, (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out); \
+  } while (0)
   if (chunks <= 1)
-    hipLaunchKernelGGL((rms_norm_kernel<1>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
-                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
+    MOE_RMS(1);
   else if (chunks <= 4)
-    hipLaunchKernelGGL((rms_norm_kernel<4>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
-                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
+    MOE_RMS(4);
   else
-    hipLaunchKernelGGL((rms_norm_kernel<16>), grid, block, 0, s, (const uint16_t*)x, (const uint16_t*)add,
-                       (const uint16_t*)w, R, C, eps, (uint16_t*)out, (uint16_t*)sum_out);
+    MOE_RMS(16);
+#undef MOE_RMS
   MOE_CHECK_LAUNCH();
   return MOE_OK;
 }
