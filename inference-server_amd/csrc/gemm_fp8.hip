@@ -522,6 +522,8 @@ int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
   if constexpr (MODE == MODE_DOWN && WM == 1 && !SHA) {
     if (KB == 3 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 3, QH>(a, max_tiles, s);
     if (KB == 4 * KS) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 4, QH>(a, max_tiles, s);
+    if constexpr (KS == 1)
+      if (KB == 6) return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 6, QH>(a, max_tiles, s);
   }
   return launch_gemm_nkw<MODE, WM, KS, DN, SHA, ROUTED, 0, QH>(a, max_tiles, s);
 }
@@ -533,9 +535,15 @@ int launch_gemm(const GemmArgs& a, int max_tiles, hipStream_t s) {
 // 62.5 / 85.3 / 109.0 / 123.2 us (gate_up 36.1 / 50.8 / 66.0 -> 33.6 / 47.5 / 61.4 us; down level).
 bool down_quantises_h(int S, int I) { return I <= kQhMaxK && !(I / MOE_GROUP == 8 && S > 16); }
 
-// 16-row down GEMM: two column slices per wave beyond 2 tokens' pairs (T=8: down 25.7 -> 24.9 us;
-// level at 1, 32 and 64 tokens); g2.a / g2.sa are bf16 h / null with qh, else hq / its scales.
+// 16-row down GEMM; g2.a / g2.sa are bf16 h / null with qh, else hq / its scales.  Quantising h
+// with 3, 4 or 6 K blocks in all: four 16-column waves per workgroup, each over the whole K (no
+// K split, so no LDS reduction or its barrier; the same 12 KB per wave at the 30B shape): 30B
+// down at 1 / 8 / 64 / 128 tokens 11.3 / 23.2 / 46.5 / 54.4 -> 10.9 / 23.0 / 45.8 / 53.8 us.
+// Otherwise a two-way K split, and two column slices per wave beyond 2 tokens' pairs (T=8: down
+// 25.7 -> 24.9 us; level at 1, 32 and 64 tokens).
 int launch_down16(const GemmArgs& g2, int S, int max_tiles, bool qh, hipStream_t s) {
+  const int KB = g2.K / MOE_GROUP;
+  if (qh && (KB == 3 || KB == 4 || KB == 6)) return launch_gemm<MODE_DOWN, 1, 1, 1, false, false, true>(g2, max_tiles, s);
   if (qh)
     return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2, false, false, true>(g2, max_tiles, s)
                   : launch_gemm<MODE_DOWN, 1, 2, 1, false, false, true>(g2, max_tiles, s);

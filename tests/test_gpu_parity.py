@@ -337,6 +337,9 @@ SHAPE_SWEEP = [
     (2, 256, 2048, 16, 4),     # the same two at I = 2048
     (6, 256, 2048, 32, 4),
     (3, 256, 1024, 16, 4),     # the down GEMM quantises h itself with 4 K blocks per wave (NKW = 4)
+    (10, 256, 384, 16, 4),     # 16-row tiles, h quantised by the down GEMM, no K split: 3 K blocks
+    (10, 256, 512, 16, 4),     # the same with 4 K blocks
+    (4, 4096, 768, 8, 2),      # the same with 6 K blocks and exact accumulation (routed slots)
     (5, 4096, 256, 8, 2),      # H > 2048: exact bf16 MFMAs on widened e4m3, 16-row tiles
     (30, 4096, 256, 10, 4),    # exact, 32-row tiles
     (60, 4096, 256, 10, 4),    # exact, 64-row tiles
