@@ -541,12 +541,16 @@ bool down_quantises_h(int S, int I) { return I <= kQhMaxK && !(I / MOE_GROUP == 
 // down at 1 / 8 / 64 / 128 tokens 11.3 / 23.2 / 46.5 / 54.4 -> 10.9 / 23.0 / 45.8 / 53.8 us.
 // Otherwise a two-way K split, and two column slices per wave beyond 2 tokens' pairs (T=8: down
 // 25.7 -> 24.9 us; level at 1, 32 and 64 tokens).
-int launch_down16(const GemmArgs& g2, int S, int max_tiles, bool qh, hipStream_t s) {
+// few_pairs (h quantised in gate_up's hand-off, up to 2 pairs per expert) with 12 K blocks: a
+// four-way K split of 3 blocks per wave, two column slices (Qwen3-235B-A22B down at 8 / 32
+// tokens 68.0 / 129.7 -> 65.3 / 126.5 us; at 64 tokens it was 2.7 us slower, so not there).
+int launch_down16(const GemmArgs& g2, int S, int max_tiles, bool qh, hipStream_t s, bool few_pairs = false) {
   const int KB = g2.K / MOE_GROUP;
   if (qh && (KB == 3 || KB == 4 || KB == 6)) return launch_gemm<MODE_DOWN, 1, 1, 1, false, false, true>(g2, max_tiles, s);
   if (qh)
     return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2, false, false, true>(g2, max_tiles, s)
                   : launch_gemm<MODE_DOWN, 1, 2, 1, false, false, true>(g2, max_tiles, s);
+  if (few_pairs && KB == 12) return launch_gemm_nkw<MODE_DOWN, 1, 4, 2, false, false, 3>(g2, max_tiles, s);
   return S > 16 ? launch_gemm<MODE_DOWN, 1, 2, 2>(g2, max_tiles, s) : launch_gemm<MODE_DOWN, 1, 2>(g2, max_tiles, s);
 }
 
@@ -573,7 +577,7 @@ int moe_gemm_block_m(int S, int E, int H, int I) {
 // Column blocks of the decode down GEMM for S pairs at tile height block_m: the width of the
 // per-token hand-off counters (tok_cnt [T, blocks]).
 int moe_down_col_blocks(int S, int H, int block_m) {
-  if (block_m == 16) return S > 16 ? H / 64 : H / 32;  // CG 2 x 16 DN columns
+  if (block_m == 16) return H / 32;  // 32-column workgroups: CG 2 x 16, or CG 1 x 32 (narrow_k)
   if (block_m == 32) return H / 128;                   // CG 4 x 32 columns
   return H / 64;                                       // CG 4 x 16 columns
 }
@@ -612,7 +616,7 @@ int moe_launch_grouped_gemms(const uint8_t* xq, const float* sx, const uint8_t* 
               nullptr, nullptr, nullptr, tok_cnt, comb, residual};
   g2.exact = moe_exact_accum(H);
   if (block_m == 16)
-    rc = launch_down16(g2, S, max_tiles, qh, s);
+    rc = launch_down16(g2, S, max_tiles, qh, s, g1.tile_cnt != nullptr);
   else if (block_m == 32)
     rc = launch_gemm<MODE_DOWN, 2, 1, 2, true>(g2, max_tiles, s);
   else
@@ -651,7 +655,7 @@ int moe_launch_grouped_gemms_routed(const uint8_t* xq, const float* sx, const ui
     rc = moe_launch_quant_act(h, S, I, hq, sh, s, MOE_PROF_QUANT_H);
     if (rc) return rc;
   }
-  return launch_down16(g2, S, S, qh, s);
+  return launch_down16(g2, S, S, qh, s, g1.tile_cnt != nullptr);
 }
 
 // The 16-row decode GEMMs on expert-bucket tiles (moe_launch_route_buckets: no sort launch): the
@@ -682,5 +686,5 @@ int moe_launch_grouped_gemms_buckets(const uint8_t* xq, const float* sx, const u
               nullptr, nullptr, nullptr, tok_cnt, comb, residual};
   g2.exact = moe_exact_accum(H);
   g2.bucket = bucket;
-  return launch_down16(g2, S, max_tiles, qh, s);
+  return launch_down16(g2, S, max_tiles, qh, s, g1.tile_cnt != nullptr);
 }
