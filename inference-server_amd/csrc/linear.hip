@@ -15,9 +15,9 @@
 // With ks > 1 each workgroup writes its fp32 partial block and linear_reduce_kernel sums the ks
 // partials of every output in chunk order (deterministic) and rounds once to bf16.
 //
-// Measured on MI355X with weights cold in HBM and graph-launched calls: 9-10 us for the q/k/v and
-// o_proj shapes at 1 to 8 rows (hipBLASLt: 12-14 us), 15-16 us at 64 rows (13 us); at 128 rows it
-// is 20 / 18 us against hipBLASLt's 15 / 12 us, 4-5 us of which is the partial-sum pass.
+// Measured on MI355X with weights cold in HBM and graph-launched calls: 10-10.7 us for the q/k/v and
+// o_proj shapes at 1 to 16 rows (hipBLASLt: 12-14 us), 16 / 13.5 us at 64 rows (12.7 / 13.3 us);
+// at 128 rows 20 / 18 us against hipBLASLt's 15 / 12 us, 4-5 us of which is the partial-sum pass.
 #include "common.h"
 
 namespace {

@@ -17,9 +17,10 @@ Per layer this is four entry points of this library plus the two projections:
 ``moe_mi355x_qk_norm_rope_append`` (q_norm, k_norm, rotary, KV-cache update),
 ``moe_mi355x_paged_attn_decode``, o_proj, and ``moe_mi355x_moe_sublayer_fp8`` (the residual add
 after the attention, post_attention_layernorm, the MoE block, the residual add).  The projections
-run on ``moe_mi355x_linear_bf16`` up to ``LINEAR_MAX_ROWS`` sequences, where it measures faster
-than hipBLASLt (9-10 us against 12-14 us per projection at 1-8 rows), and on hipBLASLt through
-``torch.nn.functional.linear`` above (15 / 12 us against 20 / 18 us at 128 rows).
+run on ``moe_mi355x_linear_bf16`` up to ``LINEAR_MAX_ROWS`` sequences, where the pair measures
+faster than hipBLASLt in a graph replay (q/k/v + o_proj 1 / 16 / 24 rows: 19.7 / 21.2 / 23.8 us
+against 26.1 / 26.4 / 26.6 us), and on hipBLASLt through ``torch.nn.functional.linear`` above
+(32 rows: 24.5 against 23.6 us).
 ``DecodeModel.capture`` records a whole step as one HIP graph, so a step costs one launch.
 """
 
@@ -32,7 +33,7 @@ import torch
 from . import kernels
 
 # Batch size up to which the decode step's projections use the library's bf16 linear kernel.
-LINEAR_MAX_ROWS = 64
+LINEAR_MAX_ROWS = 24
 
 
 def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
