@@ -123,3 +123,24 @@ def test_bf16_noalloc_and_numerics_queries(lib):
     assert int(lib.moe_mi355x_block_numerics_key(100, 384, 256, 6, 3, 1)) & 0xFFFF == 64
     # bf16 above 16 pairs per expert with H % 256 != 0: 64-row tiles
     assert int(lib.moe_mi355x_block_numerics_key(100, 384, 256, 8, 2, 0)) & 0xFFFF == 64
+
+
+def test_linear_bf16_queries_and_argument_checks(lib):
+    """The decode-step projection entry point: workspace query (the K split's fp32 partials) and
+    the checks that return before a launch."""
+    null = None
+    fake = 0x10000  # 16-byte aligned, never dereferenced on these paths
+    # batch 128 q/k/v: four K chunks of fp32 partials; one row: no split below 256-deep chunks
+    assert lib.moe_mi355x_linear_bf16_workspace_bytes(128, 5120, 2048) == 4 * 128 * 5120 * 4
+    assert lib.moe_mi355x_linear_bf16_workspace_bytes(300, 64, 128) == 0
+    assert lib.moe_mi355x_linear_bf16_workspace_bytes(8, 100, 2048) == 0   # N not a multiple of 64
+    # unsupported shapes -> MOE_ERR_INVALID_ARG (-1)
+    assert lib.moe_mi355x_linear_bf16(fake, fake, 8, 100, 2048, fake, fake, 1 << 20, null) == -1
+    assert lib.moe_mi355x_linear_bf16(fake, fake, 8, 128, 200, fake, fake, 1 << 20, null) == -1
+    assert lib.moe_mi355x_linear_bf16(fake, fake, -1, 128, 256, fake, fake, 1 << 20, null) == -1
+    # M == 0 is a successful no-op; null tensors with M > 0 are rejected
+    assert lib.moe_mi355x_linear_bf16(null, null, 0, 128, 256, null, null, 0, null) == 0
+    assert lib.moe_mi355x_linear_bf16(null, fake, 8, 128, 256, fake, fake, 1 << 20, null) == -1
+    # misaligned operand -> MOE_ERR_ALIGNMENT, missing workspace for a split -> MOE_ERR_WORKSPACE
+    assert lib.moe_mi355x_linear_bf16(fake + 2, fake, 8, 5120, 2048, fake, fake, 1 << 24, null) == -3
+    assert lib.moe_mi355x_linear_bf16(fake, fake, 128, 5120, 2048, fake, null, 0, null) == -2
