@@ -198,7 +198,8 @@ long long moe_mi355x_block_numerics_key(int T, int H, int I, int E, int k, int f
  *   num_pages                               pages in each of k_cache and v_cache
  * The KV layout is this library's; the reference keeps a contiguous per-layer cache.
  * Constraints: head_dim == 128, page_size == 16, Hq % Hkv == 0, Hq / Hkv <= 16; q, k_cache,
- * v_cache and out 16-byte aligned.
+ * v_cache and out 16-byte aligned; B * Hkv * (splits of max_pages) < 2^31 (splits of up to 64
+ * pages; the workspace query returns 0 past it).
  */
 size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages);
 int moe_mi355x_paged_attn_decode(const void* q, const void* k_cache, const void* v_cache,

@@ -394,15 +394,21 @@ int attn_pps(int B, int Hkv, int max_pages) {
   return pps;
 }
 
+// the decode grid (one workgroup per possible (sequence, kv head, split) item) and the items'
+// int indices must stay below 2^31
+bool attn_grid_ok(int B, int Hkv, int max_pages) {
+  return (long)B * Hkv * attn_max_splits(max_pages, attn_pps(B, Hkv, max_pages)) < (1L << 31);
+}
+
 bool attn_args_ok(int B, int Hq, int Hkv, int head_dim, int page_size, int max_pages, int num_pages) {
   return B > 0 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && head_dim == kHD &&
-         page_size == kPage && max_pages > 0 && num_pages >= 0;
+         page_size == kPage && max_pages > 0 && num_pages >= 0 && attn_grid_ok(B, Hkv, max_pages);
 }
 
 }  // namespace
 
 extern "C" size_t moe_mi355x_paged_attn_workspace_bytes(int B, int Hq, int Hkv, int max_pages) {
-  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_pages <= 0) return 0;
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || max_pages <= 0 || !attn_grid_ok(B, Hkv, max_pages)) return 0;
   const int pps = attn_pps(B, Hkv, max_pages);
   const long parts = (long)B * Hq * attn_max_splits(max_pages, pps);
   return moe_align_up((size_t)parts * kHD * sizeof(float), 256) + moe_align_up((size_t)parts * 2 * sizeof(float), 256);

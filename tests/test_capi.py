@@ -144,3 +144,34 @@ def test_linear_bf16_queries_and_argument_checks(lib):
     # misaligned operand -> MOE_ERR_ALIGNMENT, missing workspace for a split -> MOE_ERR_WORKSPACE
     assert lib.moe_mi355x_linear_bf16(fake + 2, fake, 8, 5120, 2048, fake, fake, 1 << 24, null) == -3
     assert lib.moe_mi355x_linear_bf16(fake, fake, 128, 5120, 2048, fake, null, 0, null) == -2
+
+
+def test_paged_attention_queries_and_argument_checks(lib):
+    """Paged attention: the workspace query (fp32 partial outputs and (max, sum) pairs per
+    (sequence, q head, split)) and the checks that return before a launch, including batches whose
+    decode grid would not fit the kernel's 32-bit item indices."""
+    null = None
+    fake = 0x10000  # 16-byte aligned, never dereferenced on these paths
+    # config 5: 128 sequences, 32 q / 4 kv heads, 512 pages -> 64-page splits, 8 per sequence
+    parts = 128 * 32 * 8
+    align = lambda n: (n + 255) // 256 * 256
+    assert lib.moe_mi355x_paged_attn_workspace_bytes(128, 32, 4, 512) == align(parts * 128 * 4) + align(parts * 2 * 4)
+    # a small batch shortens the splits (down to 8 pages) so that the grid fills more of the chip:
+    # one sequence of 64 pages -> 8 splits per head instead of 1
+    assert lib.moe_mi355x_paged_attn_workspace_bytes(1, 32, 4, 64) == align(256 * 128 * 4) + align(256 * 2 * 4)
+    # invalid shapes and grids past 2^31 items -> 0 bytes, MOE_ERR_INVALID_ARG (-1)
+    assert lib.moe_mi355x_paged_attn_workspace_bytes(128, 30, 4, 512) == 0
+    assert lib.moe_mi355x_paged_attn_workspace_bytes(1 << 20, 64, 8, 1 << 16) == 0
+    args = lambda B, Hq, Hkv, hd, ps, mp: (fake, fake, fake, fake, fake, B, Hq, Hkv, hd, ps, mp, 1 << 20,
+                                             0.088, fake, fake, 1 << 30, null)
+    assert lib.moe_mi355x_paged_attn_decode(*args(1 << 20, 64, 8, 128, 16, 1 << 16)) == -1
+    assert lib.moe_mi355x_paged_attn_decode(*args(4, 32, 4, 64, 16, 8)) == -1    # head_dim 64
+    assert lib.moe_mi355x_paged_attn_decode(*args(4, 32, 4, 128, 32, 8)) == -1   # page size 32
+    assert lib.moe_mi355x_paged_attn_decode(*args(4, 64, 2, 128, 16, 8)) == -1   # 32 q heads per kv head
+    # misaligned q -> MOE_ERR_ALIGNMENT (-3); a short workspace -> MOE_ERR_WORKSPACE (-2)
+    a = list(args(4, 32, 4, 128, 16, 8))
+    a[0] = fake + 2
+    assert lib.moe_mi355x_paged_attn_decode(*a) == -3
+    a = list(args(4, 32, 4, 128, 16, 8))
+    a[15] = 16
+    assert lib.moe_mi355x_paged_attn_decode(*a) == -2
