@@ -332,6 +332,8 @@ __device__ __forceinline__ int load_id(const void* ids, int id_bytes, int i) {
 static inline size_t moe_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 static inline bool moe_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+// a 1-D grid of n workgroups fits the launch (gridDim.x is 32-bit; kernels index workgroups as int)
+static inline bool moe_grid_fits(long n) { return n >= 0 && n < (1L << 31); }
 
 #define MOE_CHECK_LAUNCH()                          \
   do {                                              \

@@ -196,6 +196,7 @@ extern "C" int moe_mi355x_qk_norm_rope_append(const void* qkv, const void* q_nor
                     !block_tables,
                 MOE_ERR_INVALID_ARG);
   const long items = (long)B * (Hq + 2 * Hkv);
+  MOE_RETURN_IF(!moe_grid_fits((items + 3) / 4), MOE_ERR_INVALID_ARG);
   hipLaunchKernelGGL(qk_norm_rope_append_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, inv_freq, positions,
                      B, Hq, Hkv, eps, (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, block_tables,

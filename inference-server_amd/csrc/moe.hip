@@ -130,6 +130,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 int moe_launch_combine(const uint16_t* pairs, const void* ids, int id_bytes, const uint16_t* wts, int T, int k, int H,
                        int E, const uint16_t* residual, uint16_t* out, hipStream_t s) {
   const long threads = (long)T * (H / 8);
+  MOE_RETURN_IF(!moe_grid_fits((threads + 255) / 256), MOE_ERR_INVALID_ARG);
   MOE_LAUNCH(MOE_PROF_COMBINE, s, combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, pairs, ids,
              id_bytes, wts, T, k, H, E, residual, out);
   MOE_CHECK_LAUNCH();

@@ -63,6 +63,7 @@ int moe_launch_quant_act(const void* x, int R, int C, void* q, float* scales, hi
   if (R == 0) return MOE_OK;
   const long n_groups = (long)R * (C / MOE_GROUP);
   const long blocks = (n_groups + 15) / 16;
+  MOE_RETURN_IF(!moe_grid_fits(blocks), MOE_ERR_INVALID_ARG);
   MOE_LAUNCH(slot, s, quant_act_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const uint16_t*)x,
              n_groups, (uint8_t*)q, scales);
   MOE_CHECK_LAUNCH();
@@ -85,6 +86,7 @@ extern "C" int moe_mi355x_quantize_weight_fp8(const void* w, int w_dtype, int B,
   MOE_RETURN_IF(!w || !q || !scale_inv, MOE_ERR_INVALID_ARG);
   MOE_RETURN_IF(!moe_aligned16(w) || !moe_aligned16(q), MOE_ERR_ALIGNMENT);
   const long tiles = (long)B * (N / MOE_GROUP) * (K / MOE_GROUP);
+  MOE_RETURN_IF(!moe_grid_fits(tiles), MOE_ERR_INVALID_ARG);
   hipStream_t s = (hipStream_t)stream;
   if (w_dtype == 0)
     hipLaunchKernelGGL(quant_weight_kernel<uint16_t>, dim3((unsigned)tiles), dim3(256), 0, s,

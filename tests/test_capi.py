@@ -175,3 +175,14 @@ def test_paged_attention_queries_and_argument_checks(lib):
     a = list(args(4, 32, 4, 128, 16, 8))
     a[15] = 16
     assert lib.moe_mi355x_paged_attn_decode(*a) == -2
+
+
+def test_oversized_grids_are_rejected_before_launch(lib):
+    """Shapes whose 1-D launch grid would pass 2^31 workgroups return MOE_ERR_INVALID_ARG (-1)
+    instead of launching a truncated grid (no device call is made on these paths)."""
+    fake = 0x10000
+    big = (1 << 31) - 1
+    assert lib.moe_mi355x_quantize_act_fp8(fake, big, 4096, fake, fake, None) == -1
+    assert lib.moe_mi355x_quantize_weight_fp8(fake, 0, big, 4096, 4096, fake, fake, None) == -1
+    assert lib.moe_mi355x_qk_norm_rope_append(fake, fake, fake, fake, fake, big, 64, 4, 128, 1e-6, fake, fake, fake,
+                                              fake, 16, 8, 1 << 20, None) == -1
