@@ -73,6 +73,13 @@ __device__ __forceinline__ int attn_pages(int ctx, int max_pages) {
   return ctx <= 0 ? 0 : min((ctx + kPage - 1) / kPage, max_pages);
 }
 
+#ifndef MOE_ATTN_PART_BANDS
+#define MOE_ATTN_PART_BANDS 8
+#endif
+constexpr int kPartBuckets = MOE_ATTN_PART_BANDS;
+// band of a partial split of r pages (0 < r < pps): 0 for the longest
+__device__ __forceinline__ int attn_part_band(int r, int pps) { return (pps - 1 - r) * kPartBuckets / pps; }
+
 struct AttnArgs {
   const uint16_t* q;           // [B, Hq, 128] bf16
   const uint16_t* k_cache;     // [pages, Hkv, 16, 128] bf16
@@ -94,50 +101,93 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   const int lr = lane & 15, lg = lane >> 4;
   const int G = a.Hq / a.Hkv;
 
-  // workgroup -> (b, g, split): items per sequence = Hkv * ceil(pages / pps), scanned in
-  // chunks of 256 sequences (wave scans, then across the 4 waves through LDS)
-  __shared__ int s_wsum[kAttnWaves];
-  __shared__ int s_item[2];
+  // workgroup -> (b, g, split).  Items in dispatch order: every head's full splits of pps pages
+  // (sequence-major), then the partial last splits, longest first in kPartBuckets bands of their
+  // page count, so that the launch drains on short items (the slots free up one by one at the
+  // end, and with the partial splits spread through the order the last items dispatched were
+  // mostly full ones).  Split numbering (page order) is unchanged, so the merge is too.  Found
+  // by block-wide scans of the batch in chunks of 256 sequences (wave scans, then across the 4
+  // waves through LDS), one pass for the per-phase totals where the batch spans several chunks.
+  constexpr int P = 1 + kPartBuckets;
+  __shared__ int s_wsum[P][kAttnWaves];
+  __shared__ int s_item[3];
   if (threadIdx.x == 0) s_item[0] = -1;
   {
     const int item = blockIdx.x;
-    int carry = 0;
-    for (int b0 = 0; b0 < a.B; b0 += 256) {  // workgroup-uniform
+    int n[P], incl[P], before[P], tot[P], total[P], carry[P];
+    auto chunk = [&](int b0) __attribute__((always_inline)) {  // this thread's counts, then the chunk's scans
       const int bb = b0 + (int)threadIdx.x;
-      int n_it = 0;
+      int full = 0, band = -1;
       if (bb < a.B) {
         const int np = attn_pages(a.context_lens[bb], a.max_pages);
-        n_it = (np + a.pps - 1) / a.pps * a.Hkv;
+        full = np / a.pps;
+        const int r = np - full * a.pps;
+        band = r > 0 ? attn_part_band(r, a.pps) : -1;
       }
-      int incl = n_it;
+      n[0] = full * a.Hkv;
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int t = __shfl_up(incl, d);
-        if (lane >= d) incl += t;
-      }
-      if (lane == 63) s_wsum[wave] = incl;
+      for (int q = 1; q < P; ++q) n[q] = band == q - 1 ? a.Hkv : 0;
+#pragma unroll
+      for (int q = 0; q < P; ++q) incl[q] = n[q];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1)
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+          const int t = __shfl_up(incl[q], d);
+          if (lane >= d) incl[q] += t;
+        }
+      if (lane == 63)
+#pragma unroll
+        for (int q = 0; q < P; ++q) s_wsum[q][wave] = incl[q];
       __syncthreads();
-      int before = 0, total = 0;
 #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) {
-        before += w < wave ? s_wsum[w] : 0;
-        total += s_wsum[w];
+      for (int q = 0; q < P; ++q) {
+        before[q] = 0;
+        tot[q] = 0;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+          before[q] += w < wave ? s_wsum[q][w] : 0;
+          tot[q] += s_wsum[q][w];
+        }
       }
-      const int first = carry + before + incl - n_it;
-      if (n_it > 0 && item >= first && item < first + n_it) {
-        s_item[0] = bb;
-        s_item[1] = item - first;
+      __syncthreads();  // s_wsum is rewritten by the next chunk
+    };
+#pragma unroll
+    for (int q = 0; q < P; ++q) total[q] = carry[q] = 0;
+    if (a.B > 256)  // workgroup-uniform
+      for (int b0 = 0; b0 < a.B; b0 += 256) {
+        chunk(b0);
+#pragma unroll
+        for (int q = 0; q < P; ++q) total[q] += tot[q];
       }
-      carry += total;
-      __syncthreads();  // s_wsum is rewritten by the next chunk; s_item is final after the last
+    for (int b0 = 0; b0 < a.B; b0 += 256) {  // workgroup-uniform
+      chunk(b0);
+      if (a.B <= 256)
+#pragma unroll
+        for (int q = 0; q < P; ++q) total[q] = tot[q];
+      int off = 0;  // items of the earlier phases
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const int first = off + carry[q] + before[q] + incl[q] - n[q];
+        if (n[q] > 0 && item >= first && item < first + n[q]) {
+          s_item[0] = b0 + (int)threadIdx.x;
+          s_item[1] = q;
+          s_item[2] = item - first;
+        }
+        off += total[q];
+        carry[q] += tot[q];
+      }
     }
+    __syncthreads();  // s_item is final
   }
   const int b = s_item[0];
   if (b < 0) return;  // workgroup-uniform: past the last item
   const int ctx = min(a.context_lens[b], kPage * a.max_pages);
   const int n_pages = attn_pages(ctx, a.max_pages);
-  const int n_split = (n_pages + a.pps - 1) / a.pps;
-  const int g = s_item[1] / n_split, split = s_item[1] % n_split;
+  const int n_full = n_pages / a.pps;
+  const bool part = s_item[1] != 0;
+  const int g = part ? s_item[2] : s_item[2] / n_full;
+  const int split = part ? n_full : s_item[2] % n_full;
   const int p_begin = split * a.pps;
   const int p_end = min(n_pages, p_begin + a.pps);
 
