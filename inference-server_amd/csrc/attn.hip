@@ -76,9 +76,9 @@ __device__ __forceinline__ int attn_pages(int ctx, int max_pages) {
 #ifndef MOE_ATTN_PART_BANDS
 #define MOE_ATTN_PART_BANDS 8
 #endif
-constexpr int kPartBuckets = MOE_ATTN_PART_BANDS;
-// band of a partial split of r pages (0 < r < pps): 0 for the longest
-__device__ __forceinline__ int attn_part_band(int r, int pps) { return (pps - 1 - r) * kPartBuckets / pps; }
+constexpr int kPartBands = MOE_ATTN_PART_BANDS;
+// band of a partial split of r pages (0 < r < pps <= 64): 0 for the longest
+__device__ __forceinline__ int attn_part_band(int r, int pps) { return (pps - 1 - r) * kPartBands / (pps - 1); }
 
 struct AttnArgs {
   const uint16_t* q;           // [B, Hq, 128] bf16
@@ -102,81 +102,105 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   const int G = a.Hq / a.Hkv;
 
   // workgroup -> (b, g, split).  Items in dispatch order: every head's full splits of pps pages
-  // (sequence-major), then the partial last splits, longest first in kPartBuckets bands of their
+  // (sequence-major), then the partial last splits, longest first in kPartBands bands of their
   // page count, so that the launch drains on short items (the slots free up one by one at the
   // end, and with the partial splits spread through the order the last items dispatched were
   // mostly full ones).  Split numbering (page order) is unchanged, so the merge is too.  Found
-  // by block-wide scans of the batch in chunks of 256 sequences (wave scans, then across the 4
-  // waves through LDS), one pass for the per-phase totals where the batch spans several chunks.
-  constexpr int P = 1 + kPartBuckets;
-  __shared__ int s_wsum[P][kAttnWaves];
+  // in chunks of 256 sequences: a block-wide scan of the full-split items (wave scans, then
+  // across the 4 waves through LDS), and per band a wave ballot of the sequences in it (each
+  // adds Hkv items); where the batch spans several chunks, a first pass sums the totals.
+  __shared__ int s_w0[kAttnWaves];
+  __shared__ int s_cnt[kPartBands][kAttnWaves];  // sequences per band and wave, this chunk
+  __shared__ int s_tot[kPartBands], s_carry[kPartBands];  // per band: this chunk, earlier chunks
   __shared__ int s_item[3];
   if (threadIdx.x == 0) s_item[0] = -1;
   {
     const int item = blockIdx.x;
-    int n[P], incl[P], before[P], tot[P], total[P], carry[P];
-    auto chunk = [&](int b0) __attribute__((always_inline)) {  // this thread's counts, then the chunk's scans
+    int n0 = 0, incl0 = 0, before0 = 0, tot0 = 0, band = -1, rank = 0;
+    // this thread's sequence: full-split items and band; the chunk's scan and band counts
+    auto chunk = [&](int b0) __attribute__((always_inline)) {
       const int bb = b0 + (int)threadIdx.x;
-      int full = 0, band = -1;
+      int full = 0;
+      band = -1;
       if (bb < a.B) {
         const int np = attn_pages(a.context_lens[bb], a.max_pages);
         full = np / a.pps;
         const int r = np - full * a.pps;
         band = r > 0 ? attn_part_band(r, a.pps) : -1;
       }
-      n[0] = full * a.Hkv;
+      n0 = full * a.Hkv;
+      incl0 = n0;
 #pragma unroll
-      for (int q = 1; q < P; ++q) n[q] = band == q - 1 ? a.Hkv : 0;
-#pragma unroll
-      for (int q = 0; q < P; ++q) incl[q] = n[q];
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1)
-#pragma unroll
-        for (int q = 0; q < P; ++q) {
-          const int t = __shfl_up(incl[q], d);
-          if (lane >= d) incl[q] += t;
-        }
-      if (lane == 63)
-#pragma unroll
-        for (int q = 0; q < P; ++q) s_wsum[q][wave] = incl[q];
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        before[q] = 0;
-        tot[q] = 0;
-#pragma unroll
-        for (int w = 0; w < kAttnWaves; ++w) {
-          before[q] += w < wave ? s_wsum[q][w] : 0;
-          tot[q] += s_wsum[q][w];
-        }
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl0, d);
+        if (lane >= d) incl0 += t;
       }
-      __syncthreads();  // s_wsum is rewritten by the next chunk
-    };
+      if (lane == 63) s_w0[wave] = incl0;
+      const uint64_t below = (1ull << lane) - 1;
+      for (int q = 0; q < kPartBands; ++q) {  // uniform loop
+        const uint64_t m = __ballot(band == q);
+        if (lane == 0) s_cnt[q][wave] = __popcll(m);
+        if (band == q) rank = __popcll(m & below);
+      }
+      __syncthreads();
+      before0 = 0;
+      tot0 = 0;
 #pragma unroll
-    for (int q = 0; q < P; ++q) total[q] = carry[q] = 0;
-    if (a.B > 256)  // workgroup-uniform
+      for (int w = 0; w < kAttnWaves; ++w) {
+        before0 += w < wave ? s_w0[w] : 0;
+        tot0 += s_w0[w];
+      }
+      if (band >= 0)
+        for (int w = 0; w < wave; ++w) rank += s_cnt[band][w];
+      if (threadIdx.x < kPartBands) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) t += s_cnt[threadIdx.x][w];
+        s_tot[threadIdx.x] = t;
+      }
+      __syncthreads();
+    };
+    __shared__ int s_total[kPartBands];  // per band, the whole batch
+    int n_full = 0;  // full-split items of the whole batch
+    if (threadIdx.x < kPartBands) {
+      s_total[threadIdx.x] = 0;
+      s_carry[threadIdx.x] = 0;
+    }
+    if (a.B > 256) {  // workgroup-uniform
       for (int b0 = 0; b0 < a.B; b0 += 256) {
         chunk(b0);
-#pragma unroll
-        for (int q = 0; q < P; ++q) total[q] += tot[q];
+        n_full += tot0;
+        if (threadIdx.x < kPartBands) s_total[threadIdx.x] += s_tot[threadIdx.x];
       }
+      __syncthreads();
+    }
+    int carry0 = 0;
     for (int b0 = 0; b0 < a.B; b0 += 256) {  // workgroup-uniform
       chunk(b0);
-      if (a.B <= 256)
-#pragma unroll
-        for (int q = 0; q < P; ++q) total[q] = tot[q];
-      int off = 0;  // items of the earlier phases
-#pragma unroll
-      for (int q = 0; q < P; ++q) {
-        const int first = off + carry[q] + before[q] + incl[q] - n[q];
-        if (n[q] > 0 && item >= first && item < first + n[q]) {
-          s_item[0] = b0 + (int)threadIdx.x;
-          s_item[1] = q;
-          s_item[2] = item - first;
-        }
-        off += total[q];
-        carry[q] += tot[q];
+      if (a.B <= 256) {
+        n_full = tot0;
+        if (threadIdx.x < kPartBands) s_total[threadIdx.x] = s_tot[threadIdx.x];
+        __syncthreads();
       }
+      const int first = carry0 + before0 + incl0 - n0;
+      if (n0 > 0 && item >= first && item < first + n0) {
+        s_item[0] = b0 + (int)threadIdx.x;
+        s_item[1] = 0;
+        s_item[2] = item - first;
+      }
+      if (band >= 0) {
+        int off = n_full;  // items of the longer bands
+        for (int q = 0; q < band; ++q) off += s_total[q] * a.Hkv;
+        const int f = off + (s_carry[band] + rank) * a.Hkv;
+        if (item >= f && item < f + a.Hkv) {
+          s_item[0] = b0 + (int)threadIdx.x;
+          s_item[1] = 1;
+          s_item[2] = item - f;
+        }
+      }
+      carry0 += tot0;
+      __syncthreads();  // every thread has read s_carry
+      if (threadIdx.x < kPartBands) s_carry[threadIdx.x] += s_tot[threadIdx.x];
     }
     __syncthreads();  // s_item is final
   }

@@ -56,7 +56,9 @@ def run_case(pkg, dev, lens, Hq, Hkv, seed, q_std=1.0):
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
-    ref = np.stack([att.decode_attention(q[b], k, v, SCALE) for b, (k, v) in enumerate(seqs)])
+    # an empty context attends to nothing: the kernel writes zeros
+    ref = np.stack([att.decode_attention(q[b], k, v, SCALE) if len(k) else np.zeros((Hq, D), np.float32)
+                    for b, (k, v) in enumerate(seqs)])
     return got, ref
 
 
@@ -69,6 +71,21 @@ def run_case(pkg, dev, lens, Hq, Hkv, seed, q_std=1.0):
 ])
 def test_paged_attention_matches_oracle(pkg, dev, lens, Hq, Hkv):
     got, ref = run_case(pkg, dev, lens, Hq, Hkv, seed=sum(lens))
+    max_abs, mean_rel = errors(got, ref)
+    assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
+
+
+def test_paged_attention_many_sequences(pkg, dev):
+    """600 sequences: the item scan runs in three chunks of 256 (a totals pass, then the locating
+    pass); full 64-page splits, partial last splits of every length and empty contexts, so every
+    dispatch phase is populated."""
+    rng = np.random.default_rng(600)
+    lens = rng.integers(1, 1300, size=600)
+    lens[rng.random(600) < 0.05] = 0
+    lens[:63] = 16 * (64 + np.arange(1, 64)) - 5  # one full split, then a partial one of 1..63 pages
+    lens = [int(x) for x in lens]
+    got, ref = run_case(pkg, dev, lens, 32, 4, seed=600)
+    assert (got[np.array(lens) == 0] == 0).all()
     max_abs, mean_rel = errors(got, ref)
     assert max_abs <= 2e-2 and mean_rel <= 1e-2, (max_abs, mean_rel)
 
