@@ -112,18 +112,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   __shared__ int s_w0[kAttnWaves];
   __shared__ int s_cnt[kPartBands][kAttnWaves];  // sequences per band and wave, this chunk
   __shared__ int s_tot[kPartBands], s_carry[kPartBands];  // per band: this chunk, earlier chunks
-  __shared__ int s_item[3];
+  __shared__ int s_item[4];  // sequence, phase, index within it, context length
   if (threadIdx.x == 0) s_item[0] = -1;
   {
     const int item = blockIdx.x;
-    int n0 = 0, incl0 = 0, before0 = 0, tot0 = 0, band = -1, rank = 0;
+    int n0 = 0, incl0 = 0, before0 = 0, tot0 = 0, band = -1, rank = 0, cl = 0;
     // this thread's sequence: full-split items and band; the chunk's scan and band counts
     auto chunk = [&](int b0) __attribute__((always_inline)) {
       const int bb = b0 + (int)threadIdx.x;
       int full = 0;
       band = -1;
       if (bb < a.B) {
-        const int np = attn_pages(a.context_lens[bb], a.max_pages);
+        cl = a.context_lens[bb];
+        const int np = attn_pages(cl, a.max_pages);
         full = np / a.pps;
         const int r = np - full * a.pps;
         band = r > 0 ? attn_part_band(r, a.pps) : -1;
@@ -187,6 +188,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         s_item[0] = b0 + (int)threadIdx.x;
         s_item[1] = 0;
         s_item[2] = item - first;
+        s_item[3] = cl;
       }
       if (band >= 0) {
         int off = n_full;  // items of the longer bands
@@ -196,6 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
           s_item[0] = b0 + (int)threadIdx.x;
           s_item[1] = 1;
           s_item[2] = item - f;
+          s_item[3] = cl;
         }
       }
       carry0 += tot0;
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   }
   const int b = s_item[0];
   if (b < 0) return;  // workgroup-uniform: past the last item
-  const int ctx = min(a.context_lens[b], kPage * a.max_pages);
+  const int ctx = min(s_item[3], kPage * a.max_pages);  // the scan's read: no second round trip
   const int n_pages = attn_pages(ctx, a.max_pages);
   const int n_full = n_pages / a.pps;
   const bool part = s_item[1] != 0;
