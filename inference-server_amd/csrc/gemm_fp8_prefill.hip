@@ -94,11 +94,14 @@ __device__ __forceinline__ v8bf frag_half(const v8i& f, int h) {
 // feeds two v_mfma_f32_16x16x32_bf16 (lane group g supplies K chunks 2 g and 2 g + 1, the same
 // K permutation for both operands), which accumulate in fp32 in the MFMA: no scales, no FMAs.
 // EX: e4m3 operands, each 128-deep K block as four exact bf16 MFMAs on the widened codes (see
-// mfma_e4m3_exact) instead of one f8f6f4 MFMA.  A step slot takes one 32-deep quarter of one
-// weight fragment against the four activation fragments (four independent MFMAs; chaining a
-// tile's four quarters back to back stalled on each result), and the operands are widened just
-// before use, which keeps the kernel within its 256 VGPRs (widening whole fragments up front
-// spilled ~50 registers).
+// mfma_e4m3_exact) instead of one f8f6f4 MFMA.  The step runs in two halves of two weight
+// fragments each; within a half, quarter jj of the four activation fragments is widened once and
+// serves both weight fragments (a slot pair: 8 MFMAs, each of the 8 chains accumulating over jj
+// in the MFMA), so a step widens 192 code pairs per lane instead of 320 with one activation
+// widening per MFMA (the conversions, not the MFMAs, bounded that form: 235B prefill gate_up
+// 845 -> 700 us, down 439 -> 370 us, same bits).  Half 1's first slots fold half 0's chains into
+// the accumulators just before reusing their registers.  Widening whole fragments up front
+// spilled ~50 registers.
 template <int MODE, bool BF, bool EX = false>
 __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(PrefillArgs p) {
   static_assert(!(BF && EX), "exact accumulation is for e4m3 operands");
@@ -262,6 +265,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
     }                                                                                             \
     v4f t_[4];                                                                                    \
     v4f tx_[2][4];                                                                                \
+    v8bf aq_[4];                                                                                  \
     _Pragma("unroll") for (int it = 0; it < 21; ++it) {                                           \
       if (it < 16 && !EX) {                                                                       \
         const int ni = it >> 2, mi = it & 3;                                                      \
@@ -269,42 +273,80 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
         PF_PIN(t_[it & 3]);                                                                       \
       }                                                                                           \
       if (it < 16 && EX) {                                                                        \
-        /* slot (ni, jj): the jj-th 32-deep quarter of the K block for the four activation */      \
-        /* fragments, four independent exact MFMAs back to back */                                \
-        const int ni = it >> 2, jj = it & 3;                                                      \
+        /* slot (h, jj, nl): weight fragment ni = 2 h + nl, 32-deep quarter jj of the K block. */ \
+        /* The quarter of the four activation fragments is widened once per (h, jj) and shared */ \
+        /* by the slot pair; each of the pair's eight chains runs over jj in one register set. */ \
+        /* Half 1 folds half 0's chain (same registers) just before overwriting it. */           \
+        const int h = it >> 3, jj = (it >> 1) & 3, nl = it & 1, ni = 2 * h + nl;                  \
+        if (nl == 0) {                                                                            \
+          _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                      \
+            uint32_t a0_ = (uint32_t)AC[mi][2 * jj], a1_ = (uint32_t)AC[mi][2 * jj + 1];          \
+            asm volatile("" : "+v"(a0_), "+v"(a1_));                                              \
+            aq_[mi] = e4m3x8_to_bf16(a0_, a1_);                                                   \
+          }                                                                                       \
+        }                                                                                         \
         uint32_t b0_ = (uint32_t)B[ni][2 * jj], b1_ = (uint32_t)B[ni][2 * jj + 1];                \
         asm volatile("" : "+v"(b0_), "+v"(b1_));                                                  \
         const v8bf bw_ = e4m3x8_to_bf16(b0_, b1_);                                                \
         _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                        \
-          uint32_t a0_ = (uint32_t)AC[mi][2 * jj], a1_ = (uint32_t)AC[mi][2 * jj + 1];            \
-          asm volatile("" : "+v"(a0_), "+v"(a1_));                                                \
-          tx_[ni & 1][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(                              \
-              bw_, e4m3x8_to_bf16(a0_, a1_), jj == 0 ? zero4 : tx_[ni & 1][mi], 0, 0, 0);         \
-          PF_PIN(tx_[ni & 1][mi]);                                                                \
+          if (h == 1 && jj == 0) {                                                                \
+            _Pragma("unroll") for (int q = 0; q < 4; ++q)                                         \
+              acc[mi][nl][q] = fmaf(tx_[nl][mi][q], sca_[mi], acc[mi][nl][q]);                    \
+            PF_PIN(acc[mi][nl]);                                                                  \
+          }                                                                                       \
+          tx_[nl][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw_, aq_[mi], jj == 0 ? zero4 : tx_[nl][mi], 0, 0, 0); \
+          PF_PIN(tx_[nl][mi]);                                                                    \
         }                                                                                         \
       }                                                                                           \
-      switch (it) {                                                                               \
-        case 0: PF_RD_A(AN, 0, 0); break;                                                         \
-        case 1: PF_RD_A(AN, 0, 1); break;                                                         \
-        case 2: PF_RD_A(AN, 1, 0); break;                                                         \
-        case 3: PF_RD_A(AN, 1, 1); break;                                                         \
-        case 4: PF_RD_A(AN, 2, 0); break;                                                         \
-        case 5: PF_RD_B(B, 0, 0); break;                                                          \
-        case 6: PF_RD_B(B, 0, 1); break;                                                          \
-        case 7: PF_RD_A(AN, 2, 1); break;                                                         \
-        case 8: PF_RD_A(AN, 3, 0); break;                                                         \
-        case 9: PF_RD_B(B, 1, 0); break;                                                          \
-        case 10: PF_RD_B(B, 1, 1); break;                                                         \
-        case 11: PF_RD_A(AN, 3, 1); break;                                                        \
-        case 12: SN[0] = sS_[wm * 64 + lr]; break;                                                \
-        case 13: PF_RD_B(B, 2, 0); break;                                                         \
-        case 14: PF_RD_B(B, 2, 1); break;                                                         \
-        case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                           \
-        case 16: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                           \
-        case 17: PF_RD_B(B, 3, 0); break;                                                         \
-        case 18: PF_RD_B(B, 3, 1); break;                                                         \
-        case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                           \
-        default: PF_SW(WN, j1_, kb1_); break;                                                     \
+      if constexpr (EX) {                                                                         \
+        /* B fragment parts are reloaded one slot or more after their last quarter's MFMAs */   \
+        switch (it) {                                                                             \
+          case 0: PF_RD_A(AN, 0, 0); break;                                                       \
+          case 1: PF_RD_A(AN, 0, 1); break;                                                       \
+          case 2: PF_RD_A(AN, 1, 0); break;                                                       \
+          case 3: PF_RD_A(AN, 1, 1); break;                                                       \
+          case 4: PF_RD_B(B, 0, 0); break;                                                        \
+          case 5: PF_RD_B(B, 1, 0); break;                                                        \
+          case 6: PF_RD_A(AN, 2, 0); break;                                                       \
+          case 7: PF_RD_B(B, 0, 1); break;                                                        \
+          case 8: PF_RD_B(B, 1, 1); break;                                                        \
+          case 9: PF_RD_A(AN, 2, 1); break;                                                       \
+          case 10: PF_RD_A(AN, 3, 0); break;                                                      \
+          case 11: PF_RD_A(AN, 3, 1); break;                                                      \
+          case 12: SN[0] = sS_[wm * 64 + lr]; break;                                              \
+          case 13: PF_RD_B(B, 2, 0); break;                                                       \
+          case 14: PF_RD_B(B, 3, 0); break;                                                       \
+          case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                         \
+          case 16: PF_RD_B(B, 2, 1); break;                                                       \
+          case 17: PF_RD_B(B, 3, 1); break;                                                       \
+          case 18: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                         \
+          case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                         \
+          default: PF_SW(WN, j1_, kb1_); break;                                                   \
+        }                                                                                         \
+      } else {                                                                                    \
+        switch (it) {                                                                               \
+          case 0: PF_RD_A(AN, 0, 0); break;                                                         \
+          case 1: PF_RD_A(AN, 0, 1); break;                                                         \
+          case 2: PF_RD_A(AN, 1, 0); break;                                                         \
+          case 3: PF_RD_A(AN, 1, 1); break;                                                         \
+          case 4: PF_RD_A(AN, 2, 0); break;                                                         \
+          case 5: PF_RD_B(B, 0, 0); break;                                                          \
+          case 6: PF_RD_B(B, 0, 1); break;                                                          \
+          case 7: PF_RD_A(AN, 2, 1); break;                                                         \
+          case 8: PF_RD_A(AN, 3, 0); break;                                                         \
+          case 9: PF_RD_B(B, 1, 0); break;                                                          \
+          case 10: PF_RD_B(B, 1, 1); break;                                                         \
+          case 11: PF_RD_A(AN, 3, 1); break;                                                        \
+          case 12: SN[0] = sS_[wm * 64 + lr]; break;                                                \
+          case 13: PF_RD_B(B, 2, 0); break;                                                         \
+          case 14: PF_RD_B(B, 2, 1); break;                                                         \
+          case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                           \
+          case 16: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                           \
+          case 17: PF_RD_B(B, 3, 0); break;                                                         \
+          case 18: PF_RD_B(B, 3, 1); break;                                                         \
+          case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                           \
+          default: PF_SW(WN, j1_, kb1_); break;                                                     \
+        }                                                                                           \
       }                                                                                           \
       if (it == 1) PF_DMA_ONE(0, ab_, bb_, sab_, sbw_);                                           \
       if (it == 3) PF_DMA_ONE(1, ab_, bb_, sab_, sbw_);                                           \
@@ -319,13 +361,13 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
         _Pragma("unroll") for (int q = 0; q < 4; ++q) acc[mi][ni][q] = fmaf(t_[j & 3][q], sc_, acc[mi][ni][q]); \
         PF_PIN(acc[mi][ni]);                                                                      \
       }                                                                                           \
-      if (EX && it >= 4 && it <= 16 && (it & 3) == 0) {                                           \
-        /* weight fragment ni's four results, one slot after its last quarter */                  \
-        const int ni = (it >> 2) - 1;                                                             \
+      if (EX && (it == 16 || it == 17)) {                                                         \
+        /* half 1's chains (weight fragments 2 and 3), one slot after their last quarter */      \
+        const int nl = it - 16, ni = 2 + nl;                                                      \
         _Pragma("unroll") for (int mi = 0; mi < 4; ++mi) {                                        \
-          const float sc_ = (MODE == PF_GATE_UP && ni >= 2) ? scb_[mi] : sca_[mi];                \
+          const float sc_ = MODE == PF_GATE_UP ? scb_[mi] : sca_[mi];                             \
           _Pragma("unroll") for (int q = 0; q < 4; ++q)                                           \
-            acc[mi][ni][q] = fmaf(tx_[ni & 1][mi][q], sc_, acc[mi][ni][q]);                       \
+            acc[mi][ni][q] = fmaf(tx_[nl][mi][q], sc_, acc[mi][ni][q]);                           \
           PF_PIN(acc[mi][ni]);                                                                    \
         }                                                                                         \
       }                                                                                           \
