@@ -357,6 +357,51 @@ def sweep_entry(pkg, torch, dev, layer, T, steps, zipf=None):
     return entry
 
 
+def ep_share_entry(pkg, torch, dev, shape=None, e_local=16, steps=40):
+    """One GPU's share of an 8-way expert-parallel layer: E/8 local experts at the real H / I, fed
+    the rows the dispatch all-to-all would deliver (each of 8 GPUs' T tokens sends its k slots to
+    the slots' owners, so a GPU receives T k rows on average, one expert each: the experts entry
+    point with k = 1, ids uniform over the local experts).  The exchanges themselves are not
+    timed (one GPU).  Bytes: the local experts' weights and scales plus bf16 rows in and out."""
+    shape = shape or S30B
+    E, H, I = e_local, shape.H, shape.I
+    g = torch.Generator(device=dev).manual_seed(5)
+    copies = []
+    for _ in range(4):  # 4 x 75 MB rotated: more than the 256 MB last-level cache
+        w13 = (torch.randn((E, 2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q13, s13 = pkg.quantize_weight_fp8(w13)
+        del w13
+        w2 = (torch.randn((E, H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q2, s2 = pkg.quantize_weight_fp8(w2)
+        del w2
+        copies.append((q13, s13, q2, s2))
+    per_expert = shape.expert_bytes()
+    out = []
+    for T in (1, 8, 64, 128):
+        R = T * K_TOP
+        x = torch.randn((R, H), generator=g, device=dev).to(torch.bfloat16)
+        ids = torch.randint(0, E, (R, 1), generator=g, device=dev, dtype=torch.int64)
+        wts = torch.ones((R, 1), device=dev, dtype=torch.bfloat16)
+        active = int(torch.unique(ids).numel())
+        for i in range(5):
+            pkg.experts_fp8(x, ids, wts, *copies[i % 4])
+        torch.cuda.synchronize()
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for i in range(steps):
+            pkg.experts_fp8(x, ids, wts, *copies[i % 4])
+        en.record()
+        torch.cuda.synchronize()
+        us = st.elapsed_time(en) / steps * 1e3
+        nbytes = active * per_expert + 4 * R * H
+        out.append({"tokens_per_gpu": T, "rows_received": R, "local_experts": E, "active": active,
+                    "us": round(us, 2), "bytes": nbytes, "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    del copies
+    torch.cuda.empty_cache()
+    return {"workload": f"{shape.name} experts, one GPU's share of 8-way expert parallelism "
+                        f"({e_local} local experts, T*k received rows with k = 1)", "points": out}
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -650,6 +695,7 @@ def main():
         del b16
         torch.cuda.empty_cache()
         line["sweep"] = sweep
+        line["ep_share"] = ep_share_entry(pkg, torch, dev)
     if not args.no_decode_step and not args.no_sweep:
         del layer.copies[1:]
         torch.cuda.empty_cache()
