@@ -179,6 +179,20 @@ def test_experts_decode_30b(pkg, dev, w30b, T):
     _check_experts(pkg, dev, x, ids, w, *w30b)
 
 
+@pytest.mark.parametrize("R", [8, 512])
+def test_experts_ep_share_30b(pkg, dev, R):
+    """One GPU's share of 8-way expert parallelism (bench.py's ep_share entry): 16 local experts at
+    the 30B H / I, R received rows with one local expert each (k = 1); 8 rows take the 16-row
+    tiles, 512 rows the 128-row prefill tiles (S > 8 E)."""
+    E = 16
+    rng = np.random.default_rng(20 + R)
+    x = orc.gen_normal_bf16(rng, (R, 2048))
+    ids = rng.integers(0, E, size=(R, 1)).astype(np.int32)
+    w = orc.round_bf16(rng.uniform(0.25, 1.0, size=(R, 1)).astype(np.float32))
+    _check_experts(pkg, dev, x, ids, w, *gpu_weights(E, 2048, 768, dev, seed=3),
+                   idx_subset=np.arange(0, R, max(1, R // 128)))
+
+
 def test_experts_prefill_skewed_30b(pkg, dev, w30b):
     """4096-token chunk with Zipf-skewed routing; 96 random tokens checked (tokens are independent;
     tests/test_gpu_configs.py checks a token of every tile)."""
