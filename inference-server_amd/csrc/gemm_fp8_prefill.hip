@@ -324,29 +324,29 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
           default: PF_SW(WN, j1_, kb1_); break;                                                   \
         }                                                                                         \
       } else {                                                                                    \
-        switch (it) {                                                                               \
-          case 0: PF_RD_A(AN, 0, 0); break;                                                         \
-          case 1: PF_RD_A(AN, 0, 1); break;                                                         \
-          case 2: PF_RD_A(AN, 1, 0); break;                                                         \
-          case 3: PF_RD_A(AN, 1, 1); break;                                                         \
-          case 4: PF_RD_A(AN, 2, 0); break;                                                         \
-          case 5: PF_RD_B(B, 0, 0); break;                                                          \
-          case 6: PF_RD_B(B, 0, 1); break;                                                          \
-          case 7: PF_RD_A(AN, 2, 1); break;                                                         \
-          case 8: PF_RD_A(AN, 3, 0); break;                                                         \
-          case 9: PF_RD_B(B, 1, 0); break;                                                          \
-          case 10: PF_RD_B(B, 1, 1); break;                                                         \
-          case 11: PF_RD_A(AN, 3, 1); break;                                                        \
-          case 12: SN[0] = sS_[wm * 64 + lr]; break;                                                \
-          case 13: PF_RD_B(B, 2, 0); break;                                                         \
-          case 14: PF_RD_B(B, 2, 1); break;                                                         \
-          case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                           \
-          case 16: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                           \
-          case 17: PF_RD_B(B, 3, 0); break;                                                         \
-          case 18: PF_RD_B(B, 3, 1); break;                                                         \
-          case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                           \
-          default: PF_SW(WN, j1_, kb1_); break;                                                     \
-        }                                                                                           \
+        switch (it) {                                                                             \
+          case 0: PF_RD_A(AN, 0, 0); break;                                                       \
+          case 1: PF_RD_A(AN, 0, 1); break;                                                       \
+          case 2: PF_RD_A(AN, 1, 0); break;                                                       \
+          case 3: PF_RD_A(AN, 1, 1); break;                                                       \
+          case 4: PF_RD_A(AN, 2, 0); break;                                                       \
+          case 5: PF_RD_B(B, 0, 0); break;                                                        \
+          case 6: PF_RD_B(B, 0, 1); break;                                                        \
+          case 7: PF_RD_A(AN, 2, 1); break;                                                       \
+          case 8: PF_RD_A(AN, 3, 0); break;                                                       \
+          case 9: PF_RD_B(B, 1, 0); break;                                                        \
+          case 10: PF_RD_B(B, 1, 1); break;                                                       \
+          case 11: PF_RD_A(AN, 3, 1); break;                                                      \
+          case 12: SN[0] = sS_[wm * 64 + lr]; break;                                              \
+          case 13: PF_RD_B(B, 2, 0); break;                                                       \
+          case 14: PF_RD_B(B, 2, 1); break;                                                       \
+          case 15: SN[1] = sS_[wm * 64 + 16 + lr]; break;                                         \
+          case 16: SN[2] = sS_[wm * 64 + 32 + lr]; break;                                         \
+          case 17: PF_RD_B(B, 3, 0); break;                                                       \
+          case 18: PF_RD_B(B, 3, 1); break;                                                       \
+          case 19: SN[3] = sS_[wm * 64 + 48 + lr]; break;                                         \
+          default: PF_SW(WN, j1_, kb1_); break;                                                   \
+        }                                                                                         \
       }                                                                                           \
       if (it == 1) PF_DMA_ONE(0, ab_, bb_, sab_, sbw_);                                           \
       if (it == 3) PF_DMA_ONE(1, ab_, bb_, sab_, sbw_);                                           \
@@ -505,6 +505,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       // h = bf16(bf16(silu(bf16 g)) * bf16 u) in bf16, four consecutive h columns per lane and row
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
+        if (wm * 64 + mi * 16 >= rows) continue;  // the 16-row group lies past the tile (uniform)
         const int r = wm * 64 + mi * 16 + lr;
         if (r >= rows) continue;
         uint16_t* dst = p.h + (long)(row0 + r) * p.N + nb * 128 + wn * 32 + 4 * lg;
@@ -525,6 +526,10 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         float m = 0.f;
+        rmax[mi] = 0.f;
+        // a 16-row group past the tile's end computes nothing (wave-uniform): its rows are
+        // never stored, and its amax slots are read only for its own rows
+        if (wm * 64 + mi * 16 >= rows) continue;
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
@@ -545,6 +550,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       lds_wait_barrier();
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
+        if (wm * 64 + mi * 16 >= rows) continue;
         const int r = wm * 64 + mi * 16 + lr;
         const float amax = fmaxf(fmaxf(s_amax[0][r], s_amax[1][r]), fmaxf(s_amax[2][r], s_amax[3][r]));
         const float sc = amax > 0.f ? amax / MOE_FP8_MAX : 1.0f;
@@ -566,6 +572,7 @@ __global__ __launch_bounds__(P_THREADS, 1) void grouped_gemm_fp8_prefill_kernel(
       // bf16(z) at the pair's row; the combine applies the routing weight
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
+        if (wm * 64 + mi * 16 >= rows) continue;
         const int r = wm * 64 + mi * 16 + lr;
         if (r < rows) {
           const long pr = s_perm[jj & 1][r];
