@@ -109,14 +109,14 @@ S30B = Shape("qwen3-30b-a3b", 2048, 768)
 S235B = Shape("qwen3-235b-a22b", 4096, 1536)
 
 # HBM bytes per gate_up launch measured with two rocprofv3 --pmc runs of this script on the build of
-# commit 3b01990 (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy);
+# commit a71d4f3 (FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00, KiB; the factors calibrated on a 256 MiB copy);
 # commands and per-dispatch figures in profiles/grouped_gemm_hbm_traffic.md:
-#   decode 64:            FETCH 195,265 / WRITE 768 KiB
-#   prefill 4096, Zipf:   FETCH 291,484 / WRITE 25,445 KiB
-_TRAFFIC_SRC = "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, build of 3b01990)"
+#   decode 64:            FETCH 195,261 / WRITE 768 KiB
+#   prefill 4096, Zipf:   FETCH 292,772 / WRITE 25,458 KiB
+_TRAFFIC_SRC = "profiles/grouped_gemm_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, build of a71d4f3)"
 MEASURED_GATE_UP_TRAFFIC = {
-    ("qwen3-30b-a3b", 64): {"bytes": 195265 * 1024 * 2 + 768 * 1024, "source": _TRAFFIC_SRC},
-    ("qwen3-30b-a3b", 4096): {"bytes": 291484 * 1024 * 2 + 25445 * 1024, "source": _TRAFFIC_SRC},
+    ("qwen3-30b-a3b", 64): {"bytes": 195261 * 1024 * 2 + 768 * 1024, "source": _TRAFFIC_SRC},
+    ("qwen3-30b-a3b", 4096): {"bytes": 292772 * 1024 * 2 + 25458 * 1024, "source": _TRAFFIC_SRC},
 }
 
 
